@@ -1,0 +1,176 @@
+"""Benchmark of the MI355X sparse-conv hot path on one GPU.
+
+A step is one fused submanifold-conv launch over the whole synthetic workload (default: config c3, 256^3 grid,
+~390k shell voxels, Cin=Cout=256 bf16, fused bias+SiLU), with the kernel map already built (the decoders reuse one
+map for every conv of a level). Inputs are resident in HBM before timing starts. The kernel-map build (hash +
+neighbours + sort + block masks) is timed separately and reported under "extras".
+
+value = effective TFLOP/s = 2 * P * Ci * Co / time, P = active (row, offset) pairs, centre included; the masked
+implicit GEMM's padding work is not counted. The cpu_baseline leg times the CPU oracle (the same operator, fp32
+accumulation, multithreaded) on a bounded sample of rows of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "trellis2-cuda_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    try:  # cgroup v2 quota
+        q, p = open("/sys/fs/cgroup/cpu.max").read().split()
+        if q != "max":
+            n = min(n, max(1, int(int(q) / int(p))))
+    except (OSError, ValueError):
+        pass
+    return max(1, min(n, 16))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (every box has one GPU).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import spconv_amd as sp
+    from spconv_amd import workloads as W
+
+    dev = torch.device("cuda:0")
+    sp.load_library()
+    sp.set_stream(torch.cuda.current_stream())
+    cfg = W.CONFIGS[args.config]
+    t0 = time.time()
+    coords = W.shell_coords(cfg)
+    gen_s = time.time() - t0
+    if cfg.subdivide:  # c5: parents at C=128 -> kept children are the conv's rows
+        par = torch.from_numpy(coords).to(dev)
+        lg = W.keep_logits(len(coords), cfg.keep_frac, cfg.seed)
+        child, _ = sp.subdivide(par, torch.from_numpy(lg.view(np.int16)).to(dev).view(torch.float16))
+        tc = child.contiguous()
+    else:
+        tc = torch.from_numpy(coords).to(dev)
+    n = tc.shape[0]
+    ci, co = cfg.ci, cfg.co
+    g = torch.Generator(device=dev)
+    g.manual_seed(cfg.seed)
+    x = torch.randn((n, ci), generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn((co, 27, ci), generator=g, device=dev) / (27 * ci) ** 0.5).to(torch.bfloat16)
+    b = torch.randn((co,), generator=g, device=dev) * 0.1
+    res = torch.randn((n, co), generator=g, device=dev).to(torch.bfloat16) if "res" in cfg.epilogue else None
+    act = sp.ACT_SILU if "silu" in cfg.epilogue else sp.ACT_NONE
+    y = torch.empty((n, co), dtype=torch.bfloat16, device=dev)
+
+    # kernel-map build, timed separately (median of 5 after a warm-up)
+    stream = torch.cuda.current_stream()
+    map_ms = []
+    for i in range(6):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        cache = sp.build_neighbors(tc)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        if i:
+            map_ms.append(e0.elapsed_time(e1))
+    nbr, gray, srt = cache.tensors()
+    nbr_np = nbr.cpu().numpy()
+    P = int((nbr_np != -1).sum())
+    B1 = sp.spconv_cfg(n, ci, co)[0]
+    lst, seg = cache.valid(B1)
+    executed_pairs = int(sum(int(s) for s in (np.diff(seg.cpu().numpy()) *
+                                                np.minimum(B1, n - np.arange(len(seg) - 1) * B1))))
+
+    def step():
+        sp.subm_conv_fused(x, w, b, cache, residual=res, act=act, out=y)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = e0.elapsed_time(e1) / args.steps
+
+    flops = 2.0 * P * ci * co
+    tflops = flops / (ms * 1e-3) / 1e12
+    comp_bytes = n * ci * 2 + n * 27 * 4 + 27 * ci * co * 2 + co * 4 + (n * co * 2 if res is not None else 0) \
+        + n * co * 2 + n * 4
+    gbs = comp_bytes / (ms * 1e-3) / 1e9
+    mvox = n / (ms * 1e-3) / 1e6
+    wide = ci >= 256 or co >= 256
+    if wide:
+        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None}
+    else:
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        nt = cpu_threads()
+        onbr = nbr_np.view(np.uint32)
+        xs = x.float().cpu().numpy()
+        ws = w.float().cpu().numpy()
+        bs = b.cpu().numpy()
+        rs = res.float().cpu().numpy() if res is not None else None
+        rng = np.random.default_rng(0)
+        rows = rng.choice(n, size=min(n, 256), replace=False)
+        t = time.perf_counter()
+        oracle.conv(xs, ws, bs, onbr, res=rs, act=act, rows=rows, nthreads=nt)
+        pilot = time.perf_counter() - t
+        k = int(min(n, max(256, 256 * args.cpu_seconds / max(pilot, 1e-3))))
+        rows = rng.choice(n, size=k, replace=False)
+        t = time.perf_counter()
+        oracle.conv(xs, ws, bs, onbr, res=rs, act=act, rows=rows, nthreads=nt)
+        cs = time.perf_counter() - t
+        pairs = int((nbr_np[rows] != -1).sum())
+        cpu = {"value": round(2.0 * pairs * ci * co / cs / 1e12, 5), "unit": "TFLOP/s", "cores": nt,
+               "kind": "port",
+               "sample": f"{k} random rows of {n} ({pairs} active pairs), fp32 oracle conv, {cs:.1f}s",
+               "mvox_per_s": round(k / cs / 1e6, 4)}
+
+    out = {
+        "metric": "sparse-conv effective TFLOPS at 256^3 C=256 bf16 (active-pair flops)",
+        "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded union-of-shapes shell, random N(0,1) features)",
+        "config": {"workload": f"{cfg.name}: {cfg.grid}^3 shell N={n} Ci={ci} Co={co} bf16 {cfg.epilogue}",
+                   "N": n, "Ci": ci, "Co": co, "active_pairs": P, "tile_rows": B1},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extras": {"mvox_per_s": round(mvox, 2), "compulsory_GBps": round(gbs, 1),
+                   "kmap_build_ms": round(float(np.median(map_ms)), 4), "coord_gen_s": round(gen_s, 2),
+                   "executed_over_active_pairs": round(executed_pairs / max(P, 1), 4), "wall_s": round(wall, 3)},
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,80 @@
+/*
+ * spconv_amd -- C ABI of the MI355X (gfx950) submanifold sparse-convolution path.
+ *
+ * This is the drop-in boundary for the reference's sparse-conv entry points (suvadityamuk/trellis2-cuda
+ * src/spconv.h:5-16) exported the way the reference exports its pipeline to ctypes (apps/t2lib.cu:1-23):
+ * every call returns 0 on success or -1 with spc_last_error() set; calls are serialized by one mutex.
+ * All data pointers are DEVICE pointers (HIP, the library's current device) unless marked "host".
+ * Work is ordered on one stream (default: the null stream; see spc_set_stream).
+ *
+ * dtype codes follow the reference's DT enum (src/core.h:22): 0 = fp32, 1 = fp16, 2 = bf16.
+ */
+#ifndef SPCONV_AMD_H
+#define SPCONV_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { SPC_F32 = 0, SPC_F16 = 1, SPC_BF16 = 2 };
+enum { SPC_ACT_NONE = 0, SPC_ACT_SILU = 1 };
+#define SPC_EMPTY 0xffffffffu
+
+typedef struct spc_cache spc_cache; /* owns one SpConvCache (reference src/spconv.h:6-11) */
+
+/* Last error message of the calling process (reference apps/t2lib.cu:23 t2_last_error). */
+const char* spc_last_error(void);
+
+/* Make `hip_stream` (a hipStream_t, or NULL for the null stream) the stream every later call runs on.
+ * Reference: the single global stream of src/core.cu:20-28. */
+int spc_set_stream(void* hip_stream);
+
+/* Build the hash table and 27-offset neighbour map of `coords` (int32 [n,4] = (b,x,y,z), unique rows) in a
+ * W x H x D grid, plus the gray-code sorted row order.
+ * Replaces: build_neighbors (src/spconv.h:12, src/spconv.cu:38-54). */
+int spc_build_neighbors(const int32_t* coords, int64_t n, int W, int H, int D, spc_cache** out);
+
+/* Release a cache (its device buffers are freed in stream order). */
+int spc_cache_free(spc_cache* c);
+
+/* Device pointers owned by the cache: nbr u32 [n,27] (SPC_EMPTY = none), gray i32 [n] (27-bit mask),
+ * sorted i32 [n]. Any out-pointer may be NULL. Replaces the fields of SpConvCache (src/spconv.h:7-8). */
+int spc_cache_info(const spc_cache* c, int64_t* n, const uint32_t** nbr, const int32_t** gray,
+                   const int32_t** sorted);
+
+/* Per-block valid offset lists for blocks of B1 sorted rows: list (device, worst-case length 27*ceil(n/B1)),
+ * seg (device, ceil(n/B1)+1 entries, list[seg[b]:seg[b+1]] ascending). If L (host) is non-NULL the call waits
+ * for the stream and stores seg[last] there. Memoized per B1.
+ * Replaces: SpConvCache::valid (src/spconv.h:10, src/spconv.cu:56-75). */
+int spc_cache_valid(spc_cache* c, int B1, const int32_t** list, const int32_t** seg, int64_t* L);
+
+/* Tile choice for an (N, Ci, Co) conv: rows per tile/schedule block B1, channels per K stage BK, split S.
+ * Replaces: spconv_cfg (src/spconv.h:13-14, src/spconv.cu:177-221); the tile table is fixed per width. */
+int spc_conv_cfg(int64_t N, int Ci, int Co, int* B1, int* BK, int* S);
+
+/* out[N,Co] (dtype = x's) = subm_conv3d(x [N,Ci], w [Co,27,Ci], b [Co] or NULL).
+ * x and w: both SPC_F16 or both SPC_BF16; b_dtype: SPC_F32/F16/BF16. Ci % 32 == 0, Co % 64 == 0.
+ * Replaces: subm_conv (src/spconv.h:15-16, src/spconv.cu:159-175); the output buffer is the caller's. */
+int spc_subm_conv(const void* x, const void* w, const void* b, int dtype, int b_dtype, int64_t N, int Ci, int Co,
+                  spc_cache* c, void* out);
+
+/* Fused epilogue variant: out = act(conv(x) + b) [+ residual], one rounding to out_dtype (F32/F16/BF16);
+ * residual [N,Co] of res_dtype or NULL; act = SPC_ACT_NONE / SPC_ACT_SILU (silu(v) = v / (1 + exp(-v))).
+ * Replaces: subm_conv followed by the separate act_/add_ passes of src/ops.cu:79-82,105-113 (no reference
+ * entry point fuses them). */
+int spc_subm_conv_fused(const void* x, const void* w, const void* b, const void* residual, int dtype, int b_dtype,
+                        int res_dtype, int out_dtype, int act, int64_t N, int Ci, int Co, spc_cache* c, void* out);
+
+/* Child subdivision (c2s): children of each parent whose fp16 logit (logits [n,8]) is > 0, in (parent, slot)
+ * order; child_coords int32 [>= 8n, 4] and src int32 [>= 8n] receive the children, *m (host) their count
+ * (the call waits for the stream, as the reference does at src/sdec.cu:52).
+ * Replaces: SDecoder::c2s's k_c2s_count / scan / k_c2s_emit (src/sdec.cu:20-33,45-54). */
+int spc_subdivide(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
+                  int32_t* src, int64_t* m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,170 @@
+"""GPU parity of the masked implicit-GEMM conv against the fp32 CPU oracle on the same (bf16/fp16-quantized)
+inputs.
+
+Every case runs the kernel twice: with an fp32 output and with the case's output dtype.
+  * fp32 output vs the fp32 oracle: relative L2 <= 1e-5 and max-abs <= 1e-4 (well inside the stated bar of
+    rel-L2 <= 1e-3, max-abs <= 2e-2); the two differ only in the order of the fp32 accumulation.
+  * bf16/fp16 output: bit-identical to the fp32 output rounded (nearest-even) to that dtype -- the kernel rounds
+    once, in the epilogue -- and within rel-L2 <= 1e-3 of the rounded oracle, each element within
+    max(2e-2, one unit in the last place of the rounded oracle value). Rounding an fp32 result to bf16 alone costs
+    ~1.7e-3 relative L2 on N(0,1) data, and two fp32 sums that differ in the last bit can round to neighbouring
+    bf16 values (1 ulp = 0.03125 on [4, 8)), so the dtype comparison cannot be tighter than that.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import spconv_amd as sp
+from spconv_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def quantize(a, dt):
+    t = torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(TDT[dt])
+    return t, t.float().numpy()
+
+
+def ulp(a, dt):
+    """Spacing of the bf16/fp16 grid at |a| (normal range)."""
+    mant = 7 if dt == "bf16" else 10
+    e = np.floor(np.log2(np.maximum(np.abs(a), 1e-30)))
+    return np.exp2(e - mant)
+
+
+def compare(y, ref, out_dt, what=""):
+    yr = y.float().cpu().numpy()
+    assert np.isfinite(yr).all(), what
+    if out_dt != "f32":
+        ref = torch.from_numpy(ref).to(TDT[out_dt]).float().numpy()
+        tol = np.maximum(2e-2, ulp(ref, out_dt))
+        rel_bar = 1e-3
+    else:
+        tol = np.full(ref.shape, 1e-4)
+        rel_bar = 1e-5
+    rel = np.linalg.norm(yr - ref) / max(np.linalg.norm(ref), 1e-30)
+    err = np.abs(yr - ref)
+    mx = err.max() if ref.size else 0.0
+    assert rel <= rel_bar and np.all(err <= tol), f"{what}: rel-L2 {rel:.3g} max-abs {mx:.3g}"
+    return rel, mx
+
+
+def run_case(dev, c, ci, co, in_dt="bf16", out_dt="bf16", act=0, res_dt=None, bias_dt="f32", rows=None, seed=0,
+             bounds=(4096, 4096, 4096)):
+    n = len(c)
+    print(f"conv case n={n} ci={ci} co={co} in={in_dt} out={out_dt} act={act} res={res_dt}", flush=True)
+    cfg = W.Config("t", 0, 0, (0, 0), False, 0, ci, co, in_dt, "", 1000 + seed)
+    w, b = W.conv_params(cfg)
+    x = W.features(n, ci, seed + 1)
+    tx, qx = quantize(x, in_dt)
+    tw, qw = quantize(w, in_dt)
+    tb, qb = quantize(b, bias_dt)
+    tr = qr = None
+    if res_dt:
+        tr, qr = quantize(W.features(n, co, seed + 2), res_dt)
+    tc = torch.from_numpy(c).to(dev)
+    cache = sp.build_neighbors(tc, *bounds)
+    args = (tx.to(dev), tw.to(dev), tb.to(dev), cache)
+    rr = None if tr is None else tr.to(dev)
+    y32 = sp.subm_conv_fused(*args, residual=rr, act=act, out_dtype=torch.float32)
+    nbr, _, _, _ = oracle.build_neighbors(c, *bounds)
+    ref = oracle.conv(qx, qw, qb, nbr, res=qr, act=act, rows=rows)
+    sel = (lambda t: t) if rows is None else (lambda t: t[torch.from_numpy(np.asarray(rows)).to(dev)])
+    what = f"n={n} ci={ci} co={co} {in_dt}->{out_dt} act={act} res={res_dt}"
+    out = compare(sel(y32), ref, "f32", what)
+    if out_dt != "f32":
+        y = sp.subm_conv_fused(*args, residual=rr, act=act, out_dtype=TDT[out_dt])
+        assert torch.equal(y, y32.to(TDT[out_dt])), what + ": low-precision output is not round(fp32 output)"
+        out = compare(sel(y), ref, out_dt, what)
+    return out
+
+
+def shell(r, h=1.0, grid=None, seed=7):
+    g = grid or int(2 * r + 6)
+    return W.shell_coords(W.Config("s", g, 1, (r, r), False, h, 0, 0, "", "", seed, centred=True))
+
+
+@pytest.mark.parametrize("ci,co", [(32, 64), (64, 64), (128, 64), (64, 128), (96, 128), (256, 256), (128, 192)])
+def test_widths(gpu, ci, co):
+    run_case(gpu, shell(9.0), ci, co, out_dt="bf16")
+
+
+@pytest.mark.parametrize("in_dt", ["bf16", "f16"])
+@pytest.mark.parametrize("act,res_dt", [(0, None), (1, None), (0, "bf16"), (1, "f32"), (0, "f16")])
+def test_epilogues(gpu, in_dt, act, res_dt):
+    run_case(gpu, shell(7.0), 64, 128, in_dt=in_dt, out_dt=in_dt, act=act, res_dt=res_dt)
+    run_case(gpu, shell(7.0), 64, 64, in_dt=in_dt, out_dt=in_dt, act=act, res_dt=res_dt)
+
+
+def test_reference_entry_point(gpu):
+    """subm_conv (reference signature): output in x's dtype, fp16 bias like the decoder's weights."""
+    c = shell(6.0)
+    n = len(c)
+    w, b = W.conv_params(W.CONFIGS["c5"], ci=64, co=64)
+    x = W.features(n, 64, 3)
+    tx, qx = quantize(x, "f16")
+    tw, qw = quantize(w, "f16")
+    tb, qb = quantize(b, "f16")
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    y = sp.subm_conv(tx.to(gpu), tw.to(gpu), tb.to(gpu), cache)
+    assert y.dtype == torch.float16 and y.shape == (n, 64)
+    nbr, _, _, _ = oracle.build_neighbors(c)
+    compare(y, oracle.conv(qx, qw, qb, nbr), "f16")
+
+
+def test_edges(gpu):
+    # isolated voxels only (just the centre offset), tiles with one row, several batches, tight bounds
+    c = np.array([[0, 0, 0, 0], [0, 3, 3, 3], [1, 0, 0, 0], [2, 7, 7, 7]], np.int32)
+    run_case(gpu, c, 64, 64, out_dt="f32", bounds=(8, 8, 8))
+    run_case(gpu, c, 256, 128, out_dt="f32", bounds=(8, 8, 8))
+    # N not a multiple of the 128-row tile, one-voxel-wide lines, grid faces
+    g = np.stack(np.meshgrid(np.arange(5), np.arange(5), np.arange(7), indexing="ij"), -1).reshape(-1, 3)
+    c = np.concatenate([np.zeros((len(g), 1), np.int32), g.astype(np.int32)], 1)
+    run_case(gpu, c, 64, 64, out_dt="f32", bounds=(5, 5, 7))
+    # empty input
+    cache = sp.build_neighbors(torch.zeros((0, 4), dtype=torch.int32, device=gpu))
+    y = sp.subm_conv_fused(torch.zeros((0, 64), dtype=torch.bfloat16, device=gpu),
+                           torch.zeros((64, 27, 64), dtype=torch.bfloat16, device=gpu), None, cache)
+    assert y.shape == (0, 64)
+
+
+def test_bad_arguments(gpu):
+    c = shell(4.0)
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    n = len(c)
+    x = torch.zeros((n, 48), dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros((64, 27, 48), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        sp.subm_conv_fused(x, w, None, cache)
+    x = torch.zeros((n + 1, 64), dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros((64, 27, 64), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="rows"):
+        sp.subm_conv_fused(x, w, None, cache)
+    x = torch.zeros((n, 64), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="both"):
+        sp.subm_conv_fused(x, w.half(), None, cache)
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c4"])
+def test_configs_sampled_rows(gpu, name):
+    """Full-size workload on the GPU; 1500 seeded rows checked against the oracle."""
+    cfg = W.CONFIGS[name]
+    c = W.shell_coords(cfg)
+    rows = np.sort(np.random.default_rng(1).choice(len(c), size=min(1500, len(c)), replace=False))
+    act = 1 if "silu" in cfg.epilogue else 0
+    res = "bf16" if "res" in cfg.epilogue else None
+    run_case(gpu, c, cfg.ci, cfg.co, act=act, res_dt=res, rows=rows, seed=cfg.seed)
+
+
+def test_c5_children(gpu):
+    cfg = W.CONFIGS["c5"]
+    par = W.shell_coords(cfg)
+    tc = torch.from_numpy(par).to(gpu)
+    lg = W.keep_logits(len(par), cfg.keep_frac, cfg.seed)
+    gc, _ = sp.subdivide(tc, torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16))
+    c = gc.cpu().numpy()
+    rows = np.sort(np.random.default_rng(2).choice(len(c), size=1500, replace=False))
+    run_case(gpu, c, cfg.ci, cfg.co, act=1, rows=rows, seed=cfg.seed)

@@ -1,0 +1,109 @@
+"""GPU parity of the hash table, 27-offset kernel map, gray-code sorted order, valid lists and subdivision:
+bit-exact against the CPU oracle (and a hand-derived known answer) on the same coordinates."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import spconv_amd as sp
+from spconv_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+_coords_cache = {}
+
+
+def coords(name):
+    if name not in _coords_cache:
+        if name == "c5_children":
+            cfg = W.CONFIGS["c5"]
+            par = coords("c5")
+            oc, _ = oracle.subdivide(par, W.keep_logits(len(par), cfg.keep_frac, cfg.seed))
+            _coords_cache[name] = oc
+        else:
+            _coords_cache[name] = W.shell_coords(W.CONFIGS[name])
+    return _coords_cache[name]
+
+
+def gpu_map(c, dev, bounds=(4096, 4096, 4096)):
+    t = torch.from_numpy(np.ascontiguousarray(c, np.int32)).to(dev)
+    cache = sp.build_neighbors(t, *bounds)
+    nbr, gray, srt = cache.tensors()
+    return cache, nbr.cpu().numpy().view(np.uint32), gray.cpu().numpy(), srt.cpu().numpy()
+
+
+def check_map(c, dev, bounds=(4096, 4096, 4096), B1s=(32, 128)):
+    print(f"kmap case n={len(c)} bounds={bounds}", flush=True)
+    cache, nbr, gray, srt = gpu_map(c, dev, bounds)
+    onbr, ogray, _, osrt = oracle.build_neighbors(c, *bounds)
+    np.testing.assert_array_equal(nbr, onbr)
+    np.testing.assert_array_equal(gray, ogray)
+    np.testing.assert_array_equal(srt, osrt)
+    for B1 in B1s:
+        lst, seg = cache.valid(B1)
+        olst, oseg = oracle.valid(ogray, osrt, B1)
+        np.testing.assert_array_equal(seg.cpu().numpy(), oseg)
+        np.testing.assert_array_equal(lst.cpu().numpy(), olst)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5", "c5_children", "c4"])
+def test_kmap_configs(gpu, name):
+    check_map(coords(name), gpu, B1s=(32, 128, 1000))
+
+
+def test_kmap_known_answer(gpu):
+    c = np.array([[0, 1, 1, 1], [0, 1, 1, 2], [0, 2, 1, 1], [0, 5, 5, 5]], np.int32)
+    cache, nbr, gray, srt = gpu_map(c, gpu, (8, 8, 8))
+    exp = np.full((4, 27), 0xFFFFFFFF, np.uint32)
+    exp[0, [13, 14, 22]] = [0, 1, 2]
+    exp[1, [12, 13, 21]] = [0, 1, 2]
+    exp[2, [4, 5, 13]] = [0, 1, 2]
+    exp[3, 13] = 3
+    np.testing.assert_array_equal(nbr, exp)
+    np.testing.assert_array_equal(srt, [2, 3, 1, 0])
+    lst, seg = cache.valid(2)
+    np.testing.assert_array_equal(lst.cpu().numpy(), [4, 5, 13, 12, 13, 14, 21, 22])
+    np.testing.assert_array_equal(seg.cpu().numpy(), [0, 3, 8])
+
+
+def test_kmap_edges(gpu):
+    # empty set
+    cache, nbr, gray, srt = gpu_map(np.zeros((0, 4), np.int32), gpu)
+    assert nbr.shape == (0, 27) and len(srt) == 0
+    lst, seg = cache.valid(128)
+    assert seg.cpu().tolist() == [0]
+    # one voxel at the grid corner
+    check_map(np.array([[0, 0, 0, 0]], np.int32), gpu, (4, 4, 4), B1s=(1, 128))
+    # several batches, neighbours cut by tight bounds, voxels on every face of the box
+    c = W.shell_coords(W.Config("e", 12, 1, (5, 5), False, 1.0, 8, 8, "f32", "bias", 3, centred=True))
+    cs = []
+    for b in range(3):
+        cc = c.copy()
+        cc[:, 0] = b
+        cs.append(cc)
+    c = np.concatenate(cs)
+    check_map(c, gpu, (12, 12, 12), B1s=(1, 3, 64, 128))
+    # a full dense block: every interior voxel has all 27 neighbours, ties everywhere in the sort
+    g = np.stack(np.meshgrid(np.arange(9), np.arange(9), np.arange(9), indexing="ij"), -1).reshape(-1, 3)
+    c = np.concatenate([np.zeros((len(g), 1), np.int32), g.astype(np.int32)], 1)
+    check_map(c, gpu, (9, 9, 9))
+
+
+def test_kmap_random_permutation(gpu):
+    # row order is not Morton: the stable sort must still reproduce ties in row order
+    c = coords("c2").copy()
+    c = c[np.random.default_rng(0).permutation(len(c))]
+    check_map(c, gpu)
+
+
+@pytest.mark.parametrize("name", ["c1", "c5"])
+def test_subdivide(gpu, name):
+    par = coords(name)
+    lg = W.keep_logits(len(par), 0.35, 11)
+    lg[0, :] = np.array([-0.0, np.nan, np.inf, 6e-8, -6e-8, 0.0, -np.inf, 1.0], np.float16)
+    oc, osrc = oracle.subdivide(par, lg)
+    tc = torch.from_numpy(par).to(gpu)
+    tl = torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16)
+    gc, gs = sp.subdivide(tc, tl)
+    np.testing.assert_array_equal(gc.cpu().numpy(), oc)
+    np.testing.assert_array_equal(gs.cpu().numpy(), osrc)

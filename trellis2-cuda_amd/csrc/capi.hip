@@ -1,0 +1,127 @@
+// extern "C" boundary over the C++ API, with the reference's embedding convention (apps/t2lib.cu:1-23):
+// 0 / -1 + last error string, all calls serialized by one mutex, exceptions never cross the ABI.
+#include <exception>
+#include <mutex>
+
+#include "../../include/spconv_amd.h"
+#include "spconv.h"
+
+#define SPC_API extern "C" __attribute__((visibility("default")))
+
+struct spc_cache {
+  SpConvCache c;
+};
+
+namespace {
+std::mutex mu;
+std::string last_error;
+
+template <class F>
+int guarded(F&& f) {
+  std::lock_guard<std::mutex> lk(mu);
+  try {
+    f();
+    return 0;
+  } catch (const std::exception& e) {
+    last_error = e.what();
+  } catch (...) {
+    last_error = "unknown error";
+  }
+  return -1;
+}
+DT float_dt(int d, const char* what) {
+  REQ(d == SPC_F32 || d == SPC_F16 || d == SPC_BF16, "%s dtype code %d", what, d);
+  return (DT)d;
+}
+}  // namespace
+
+SPC_API const char* spc_last_error(void) { return last_error.c_str(); }
+
+SPC_API int spc_set_stream(void* s) {
+  return guarded([&] { set_stream((hipStream_t)s); });
+}
+
+SPC_API int spc_build_neighbors(const int32_t* coords, int64_t n, int W, int H, int D, spc_cache** out) {
+  return guarded([&] {
+    REQ(out, "out is null");
+    REQ(n >= 0 && (n == 0 || coords), "coords null or n < 0");
+    auto h = std::make_unique<spc_cache>();
+    h->c = build_neighbors(borrow(coords, {n, 4}, I32), W, H, D);
+    *out = h.release();
+  });
+}
+
+SPC_API int spc_cache_free(spc_cache* c) {
+  return guarded([&] { delete c; });
+}
+
+SPC_API int spc_cache_info(const spc_cache* c, int64_t* n, const uint32_t** nbr, const int32_t** gray,
+                           const int32_t** sorted) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    if (n) *n = c->c.N;
+    if (nbr) *nbr = c->c.nbr.ptr<uint32_t>();
+    if (gray) *gray = c->c.gray.ptr<int32_t>();
+    if (sorted) *sorted = c->c.sorted.ptr<int32_t>();
+  });
+}
+
+SPC_API int spc_cache_valid(spc_cache* c, int B1, const int32_t** list, const int32_t** seg, int64_t* L) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    auto& v = c->c.valid(B1);
+    if (list) *list = v.first.ptr<int32_t>();
+    if (seg) *seg = v.second.ptr<int32_t>();
+    if (L) {
+      i64 nb = cdiv(c->c.N, B1);
+      *L = (int64_t)to_host_vec<int32_t>(v.second.slice0(nb, nb + 1))[0];
+    }
+  });
+}
+
+SPC_API int spc_conv_cfg(int64_t N, int Ci, int Co, int* B1, int* BK, int* S) {
+  return guarded([&] {
+    SpConvCfg k = spconv_cfg((int)N, Ci, Co);
+    if (B1) *B1 = k.B1;
+    if (BK) *BK = k.BK;
+    if (S) *S = k.S;
+  });
+}
+
+SPC_API int spc_subm_conv_fused(const void* x, const void* w, const void* b, const void* residual, int dtype,
+                                int b_dtype, int res_dtype, int out_dtype, int act, int64_t N, int Ci, int Co,
+                                spc_cache* c, void* out) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    REQ(N >= 0 && Ci > 0 && Co > 0, "N=%lld Ci=%d Co=%d", (long long)N, Ci, Co);
+    REQ(N == 0 || (x && w && out), "null x/w/out");
+    DT dt = float_dt(dtype, "x/w");
+    REQ(dt != F32, "x/w must be fp16 or bf16");
+    Tensor tx = borrow(x, {N, Ci}, dt), tw = borrow(w, {Co, 27, Ci}, dt);
+    Tensor tb, tr, to = borrow(out, {N, Co}, float_dt(out_dtype, "out"));
+    if (b) tb = borrow(b, {Co}, float_dt(b_dtype, "bias"));
+    if (residual) tr = borrow(residual, {N, Co}, float_dt(res_dtype, "residual"));
+    if (N == 0) to.sh = {0, Co};
+    subm_conv_fused(tx, tw, b ? &tb : nullptr, residual ? &tr : nullptr, act, c->c, to);
+  });
+}
+
+SPC_API int spc_subm_conv(const void* x, const void* w, const void* b, int dtype, int b_dtype, int64_t N, int Ci,
+                          int Co, spc_cache* c, void* out) {
+  return spc_subm_conv_fused(x, w, b, nullptr, dtype, b_dtype, SPC_F32, dtype, SPC_ACT_NONE, N, Ci, Co, c, out);
+}
+
+SPC_API int spc_subdivide(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
+                          int32_t* src, int64_t* m) {
+  return guarded([&] {
+    REQ(m, "m is null");
+    REQ(n >= 0 && (n == 0 || (coords && logits_f16 && child_coords && src)), "null argument");
+    Subdivision s = subdivide(borrow(coords, {n, 4}, I32), borrow(logits_f16, {n, 8}, F16));
+    i64 k = s.coords.size(0);
+    if (k) {
+      CK(hipMemcpyAsync(child_coords, s.coords.p, (size_t)k * 16, hipMemcpyDeviceToDevice, stream()));
+      CK(hipMemcpyAsync(src, s.src.p, (size_t)k * 4, hipMemcpyDeviceToDevice, stream()));
+    }
+    *m = k;
+  });
+}

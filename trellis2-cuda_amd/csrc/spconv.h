@@ -1,0 +1,49 @@
+// Submanifold 3x3x3 sparse convolution on MI355X: the C++ API of the reference's src/spconv.h:1-16, kept
+// call-compatible so the sparse decoders (reference src/sdec.cu:15-18, 55, 92) can call it unchanged.
+#pragma once
+#include <map>
+#include <utility>
+
+#include "core.h"
+
+// Neighbour cache for one coordinate set (reference src/spconv.h:5-11).
+//   nbr    [N,27] u32, 0xffffffff = no neighbour, offset v <-> (dx,dy,dz) = (v/9-1, v/3%3-1, v%3-1)
+//   gray   [N] i32   27-bit neighbour mask
+//   sorted [N] i32   stable ascending order of the gray-decoded mask (ties keep row order)
+//   vk     B1 -> (valid offset list, segment offsets [ceil(N/B1)+1]); list is allocated at its worst case
+//          27*ceil(N/B1) (no host sync); its used length is seg[ceil(N/B1)].
+struct SpConvCache {
+  int N = 0;
+  Tensor nbr, gray, sorted;
+  std::map<int, std::pair<Tensor, Tensor>> vk;
+  const std::pair<Tensor, Tensor>& valid(int B1);
+  // Per-block OR of the neighbour masks over B1 consecutive sorted rows: the conv kernel's schedule. The set
+  // bits of masks[b] are exactly list[seg[b]:seg[b+1]].
+  std::map<int, Tensor> masks;
+  const Tensor& block_masks(int B1);
+};
+SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D);  // coords int32 [N,4] (b,x,y,z)
+
+// Tile choice. The reference replays FlexGEMM's autotune table (src/spconv.cu:177-221); here the tile is fixed
+// per channel width (B1 = rows per tile and per schedule block, BK = channels per K stage, S = 1).
+struct SpConvCfg {
+  int B1, BK, S;
+};
+SpConvCfg spconv_cfg(int N, int Ci, int Co);
+
+// y = subm_conv3d(x, w, b): x fp16/bf16 [N,Ci], w same dtype [Co,27,Ci], b fp16/bf16/fp32 [Co] or null.
+// Returns [N,Co] in x's dtype; fp32 accumulation, bias added to the fp32 sum before the single rounding.
+Tensor subm_conv(const Tensor& x, const Tensor& w, const Tensor* b, SpConvCache& c);
+
+enum SpAct : int { ACT_NONE = 0, ACT_SILU = 1 };
+// Fused epilogue: out[i] = act(sum_v W_v x[nbr[i,v]] + b) [+ residual[i]], rounded once to out's dtype.
+// residual may be null; out must be a defined [N,Co] tensor of dtype F32, F16 or BF16.
+void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Tensor* residual, int act,
+                     SpConvCache& c, Tensor& out);
+
+// Child subdivision of a sparse level (reference src/sdec.cu:20-57): children of each parent whose fp16 logit is
+// > 0, in (parent, slot) order, coords (b, 2x+(s&1), 2y+(s>>1&1), 2z+(s>>2&1)), src = parent*8+s.
+struct Subdivision {
+  Tensor coords, src;  // int32 [M,4], int32 [M]
+};
+Subdivision subdivide(const Tensor& coords, const Tensor& logits_f16);

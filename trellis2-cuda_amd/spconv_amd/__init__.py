@@ -1,0 +1,208 @@
+"""Python host binding of libspconv_amd.so (the C ABI declared in include/spconv_amd.h), over ctypes.
+
+PyTorch is used only for device memory and the stream; every computation runs in the HIP library. There is no
+CPU or PyTorch fallback: if the library is missing, loading raises.
+
+Mirrors the reference's C++ operator interface (suvadityamuk/trellis2-cuda src/spconv.h:5-16):
+    build_neighbors(coords, W, H, D) -> SpConvCache    (src/spconv.cu:38-54)
+    SpConvCache.valid(B1) -> (list, seg)               (src/spconv.cu:56-75)
+    spconv_cfg(N, Ci, Co) -> (B1, BK, S)               (src/spconv.cu:177-221)
+    subm_conv(x, w, b, cache) -> y                     (src/spconv.cu:159-175)
+plus subm_conv_fused (bias + SiLU / residual epilogue) and subdivide (src/sdec.cu:20-57).
+Errors raise RuntimeError carrying spc_last_error() (the reference's t2_last_error convention, apps/t2lib.cu:23).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "libspconv_amd.so")
+
+F32, F16, BF16 = 0, 1, 2
+ACT_NONE, ACT_SILU = 0, 1
+EMPTY = 0xFFFFFFFF
+
+# the C ABI's exported symbols (every declaration of include/spconv_amd.h)
+SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_cache_free", "spc_cache_info",
+           "spc_cache_valid", "spc_conv_cfg", "spc_subm_conv", "spc_subm_conv_fused", "spc_subdivide")
+
+_lib = None
+
+
+def load_library():
+    """Load (once) and prototype the C ABI. Raises OSError if the library has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise OSError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() (make -C trellis2-cuda_amd)")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    PP = ctypes.POINTER(ctypes.c_void_p)
+    L.spc_last_error.restype = ctypes.c_char_p
+    L.spc_last_error.argtypes = []
+    L.spc_set_stream.argtypes = [P]
+    L.spc_build_neighbors.argtypes = [P, I64, I, I, I, PP]
+    L.spc_cache_free.argtypes = [P]
+    L.spc_cache_info.argtypes = [P, ctypes.POINTER(I64), PP, PP, PP]
+    L.spc_cache_valid.argtypes = [P, I, PP, PP, ctypes.POINTER(I64)]
+    L.spc_conv_cfg.argtypes = [I64, I, I, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)]
+    L.spc_subm_conv.argtypes = [P, P, P, I, I, I64, I, I, P, P]
+    L.spc_subm_conv_fused.argtypes = [P, P, P, P, I, I, I, I, I, I64, I, I, P, P]
+    L.spc_subdivide.argtypes = [P, P, I64, P, P, ctypes.POINTER(I64)]
+    for name in SYMBOLS:
+        if name != "spc_last_error":
+            getattr(L, name).restype = I
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(load_library().spc_last_error().decode(errors="replace"))
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dt(t) -> int:
+    torch = _torch()
+    m = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+    if t.dtype not in m:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    return m[t.dtype]
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("tensor must be on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def set_stream(stream=None) -> None:
+    """Run later calls on a torch.cuda.Stream (None = torch's current stream)."""
+    torch = _torch()
+    s = torch.cuda.current_stream() if stream is None else stream
+    _check(load_library().spc_set_stream(ctypes.c_void_p(s.cuda_stream)))
+
+
+class SpConvCache:
+    """Owns one neighbour cache (nbr/gray/sorted + memoized valid lists); freed on garbage collection."""
+
+    def __init__(self, handle, n, device):
+        self._h = handle
+        self.N = n
+        self.device = device
+
+    def __del__(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.spc_cache_free(self._h)
+            self._h = None
+
+    def _view(self, ptr, shape, dtype):
+        torch = _torch()
+        numel = 1
+        for s in shape:
+            numel *= s
+        if numel == 0:
+            return torch.empty(shape, dtype=dtype, device=self.device)
+        # copy out of the library-owned buffer (the cache keeps ownership)
+        out = torch.empty(shape, dtype=dtype, device=self.device)
+        _memcpy_d2d(out.data_ptr(), ptr, out.numel() * out.element_size())
+        return out
+
+    def tensors(self):
+        """(nbr int32 [N,27] with -1 = EMPTY, gray int32 [N], sorted int32 [N]) as new torch tensors."""
+        torch = _torch()
+        n = ctypes.c_int64()
+        nbr, gray, srt = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        _check(load_library().spc_cache_info(self._h, ctypes.byref(n), ctypes.byref(nbr), ctypes.byref(gray),
+                                             ctypes.byref(srt)))
+        N = n.value
+        return (self._view(nbr.value, (N, 27), torch.int32), self._view(gray.value, (N,), torch.int32),
+                self._view(srt.value, (N,), torch.int32))
+
+    def valid(self, B1: int):
+        """(list int32 [L], seg int32 [ceil(N/B1)+1]) as new torch tensors."""
+        torch = _torch()
+        lst, seg, L = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int64()
+        _check(load_library().spc_cache_valid(self._h, B1, ctypes.byref(lst), ctypes.byref(seg), ctypes.byref(L)))
+        nb = (self.N + B1 - 1) // B1
+        return self._view(lst.value, (L.value,), torch.int32), self._view(seg.value, (nb + 1,), torch.int32)
+
+
+_hip = None
+
+
+def _memcpy_d2d(dst: int, src: int, nbytes: int) -> None:
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        _hip.hipMemcpy.restype = ctypes.c_int
+        _hip.hipDeviceSynchronize.restype = ctypes.c_int
+    _hip.hipDeviceSynchronize()  # the library may run on a stream other than torch's
+    rc = _hip.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), ctypes.c_size_t(nbytes), 3)
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy failed ({rc})")
+
+
+def build_neighbors(coords, W: int = 4096, H: int = 4096, D: int = 4096) -> SpConvCache:
+    torch = _torch()
+    if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
+        raise ValueError("coords must be int32 [N,4]")
+    h = ctypes.c_void_p()
+    _check(load_library().spc_build_neighbors(_ptr(coords), coords.shape[0], W, H, D, ctypes.byref(h)))
+    return SpConvCache(h, coords.shape[0], coords.device)
+
+
+def spconv_cfg(N: int, Ci: int, Co: int):
+    b1, bk, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _check(load_library().spc_conv_cfg(N, Ci, Co, ctypes.byref(b1), ctypes.byref(bk), ctypes.byref(s)))
+    return b1.value, bk.value, s.value
+
+
+def subm_conv_fused(x, w, b, cache: SpConvCache, residual=None, act: int = ACT_NONE, out=None, out_dtype=None):
+    """out = act(subm_conv3d(x, w) + b) [+ residual]; w is [Co,27,Ci] (= torch [Co,3,3,3,Ci].view)."""
+    torch = _torch()
+    N, Ci = x.shape
+    Co = w.shape[0]
+    if w.dtype != x.dtype:  # the C ABI carries one dtype code for x and w
+        raise ValueError(f"x and w must both be bf16 or both fp16 (x {x.dtype}, w {w.dtype})")
+    if out is None:
+        out = torch.empty((N, Co), dtype=out_dtype or x.dtype, device=x.device)
+    _check(load_library().spc_subm_conv_fused(
+        _ptr(x), _ptr(w), _ptr(b), _ptr(residual), _dt(x), _dt(b) if b is not None else F32,
+        _dt(residual) if residual is not None else F32, _dt(out), act, N, Ci, Co, cache._h, _ptr(out)))
+    return out
+
+
+def subm_conv(x, w, b, cache: SpConvCache):
+    """y = subm_conv3d(x, w, b) in x's dtype (reference subm_conv, src/spconv.cu:159-175)."""
+    torch = _torch()
+    N, Ci = x.shape
+    Co = w.shape[0]
+    if w.dtype != x.dtype:
+        raise ValueError(f"x and w must both be bf16 or both fp16 (x {x.dtype}, w {w.dtype})")
+    y = torch.empty((N, Co), dtype=x.dtype, device=x.device)
+    _check(load_library().spc_subm_conv(_ptr(x), _ptr(w), _ptr(b), _dt(x), _dt(b) if b is not None else F32,
+                                        N, Ci, Co, cache._h, _ptr(y)))
+    return y
+
+
+def subdivide(coords, logits_f16):
+    """(child coords int32 [M,4], src int32 [M]) for children whose fp16 logit is > 0."""
+    torch = _torch()
+    n = coords.shape[0]
+    cc = torch.empty((max(8 * n, 1), 4), dtype=torch.int32, device=coords.device)
+    src = torch.empty((max(8 * n, 1),), dtype=torch.int32, device=coords.device)
+    m = ctypes.c_int64()
+    _check(load_library().spc_subdivide(_ptr(coords), _ptr(logits_f16), n, _ptr(cc), _ptr(src), ctypes.byref(m)))
+    return cc[:m.value], src[:m.value]

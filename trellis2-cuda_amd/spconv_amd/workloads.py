@@ -1,0 +1,206 @@
+"""Seeded synthetic sparse-voxel workloads (the five benchmark configurations).
+
+Every active set is the thin shell ``|sdf(p)| <= h`` of a union of spheres or ellipsoids, evaluated at integer
+voxel positions ``p`` of a ``G^3`` grid, with ``sdf = min_i f_i`` and
+
+    f_i(p) = (|(p - c_i) / a_i| - 1) * min(a_i)        (exact signed distance for a sphere, a_i = (r, r, r))
+
+Coordinates are int32 ``(b=0, x, y, z)`` rows, unique, sorted by 3-D Morton code (x in the lowest interleaved
+bit), which is the layout the reference's decoders hand to ``build_neighbors`` (coords from an occupancy grid,
+``src/ssdec.cu:78-90``). Candidate voxels are enumerated column by column per shape (for each (x, y) the set of
+z with ``|f_i| <= h`` is at most two intervals), so a 1024^3 grid is never materialised: any voxel of the
+union's shell has ``|f_i| <= h`` for the minimising shape, so the union of per-shape candidate sets is a
+superset that is then filtered exactly.
+"""
+from __future__ import annotations
+
+import dataclasses
+import numpy as np
+
+
+@dataclasses.dataclass(frozen=True)
+class Config:
+    name: str
+    grid: int
+    n_shapes: int
+    radii: tuple          # (min, max) of the radius / semi-axes
+    ellipsoids: bool      # half of the shapes get independent semi-axes
+    half_thickness: float
+    ci: int
+    co: int
+    dtype: str            # "f32" or "bf16"
+    epilogue: str         # "bias", "bias+res", "bias+silu"
+    seed: int
+    centred: bool = False
+    subdivide: bool = False
+    keep_frac: float = 0.0
+
+
+# The five BASELINE configurations. Shape counts, radii and dtypes are the stated ones; the half-thickness h is
+# chosen per config so the voxel count lands near the stated size (counts are whatever the seed gives).
+CONFIGS = {
+    "c1": Config("c1", 32, 1, (12, 12), False, 1.5, 32, 32, "f32", "bias", 1001, centred=True),
+    "c2": Config("c2", 64, 6, (8, 20), False, 2.35, 768, 768, "bf16", "bias+res", 1002),
+    "c3": Config("c3", 256, 12, (20, 90), True, 0.8, 256, 256, "bf16", "bias+silu", 1003),
+    "c4": Config("c4", 1024, 16, (80, 350), False, 0.35, 64, 64, "bf16", "bias+res", 1004),
+    "c5": Config("c5", 512, 12, (40, 170), False, 0.6, 128, 64, "bf16", "bias+silu", 1005,
+                 subdivide=True, keep_frac=0.35),
+}
+
+
+def _shapes(cfg: Config, rng: np.random.Generator):
+    """Centres (n,3) float64 and semi-axes (n,3) float64."""
+    n = cfg.n_shapes
+    if cfg.centred:
+        cen = np.full((n, 3), cfg.grid / 2.0)
+    else:
+        cen = rng.uniform(0, cfg.grid, size=(n, 3))
+    lo, hi = cfg.radii
+    r = rng.uniform(lo, hi, size=(n, 1)) * np.ones((1, 3))
+    if cfg.ellipsoids:
+        ax = rng.uniform(lo, hi, size=(n, 3))
+        odd = np.arange(n) % 2 == 1
+        r[odd] = ax[odd]
+    return cen, r
+
+
+def _f(p: np.ndarray, c: np.ndarray, a: np.ndarray) -> np.ndarray:
+    q = (p - c) / a
+    return (np.sqrt((q * q).sum(-1)) - 1.0) * a.min()
+
+
+def _candidates(grid, c, a, h):
+    """All integer voxels of the grid with |f(p)| <= h for one shape ."""
+    m = a.min()
+    lo = max(0.0, 1.0 - h / m)
+    hi = 1.0 + h / m
+    x0, x1 = max(0, int(np.floor(c[0] - a[0] * hi))), min(grid - 1, int(np.ceil(c[0] + a[0] * hi)))
+    y0, y1 = max(0, int(np.floor(c[1] - a[1] * hi))), min(grid - 1, int(np.ceil(c[1] + a[1] * hi)))
+    if x0 > x1 or y0 > y1:
+        return np.zeros((0, 3), np.int64)
+    xs, ys = np.meshgrid(np.arange(x0, x1 + 1), np.arange(y0, y1 + 1), indexing="ij")
+    xs, ys = xs.ravel(), ys.ravel()
+    qxy = ((xs - c[0]) / a[0]) ** 2 + ((ys - c[1]) / a[1]) ** 2
+    keep = qxy <= hi * hi
+    xs, ys, qxy = xs[keep], ys[keep], qxy[keep]
+    outer = np.sqrt(np.maximum(hi * hi - qxy, 0.0)) * a[2]
+    inner = np.sqrt(np.maximum(lo * lo - qxy, 0.0)) * a[2]
+    has_hole = qxy < lo * lo
+    out = []
+    # upper interval [c + inner, c + outer] and lower [c - outer, c - inner]; a column with no hole is one interval
+    for sgn in (1, -1):
+        if sgn == 1:
+            za = np.where(has_hole, c[2] + inner, c[2] - outer)
+            zb = c[2] + outer
+        else:
+            za = c[2] - outer
+            zb = c[2] - inner
+            sel = has_hole
+            za, zb = za[sel], zb[sel]
+        xx = xs if sgn == 1 else xs[has_hole]
+        yy = ys if sgn == 1 else ys[has_hole]
+        za = np.clip(np.floor(za), 0, grid - 1).astype(np.int64)
+        zb = np.clip(np.ceil(zb), 0, grid - 1).astype(np.int64)
+        cnt = np.maximum(zb - za + 1, 0)
+        tot = int(cnt.sum())
+        if tot == 0:
+            continue
+        rep_x = np.repeat(xx, cnt)
+        rep_y = np.repeat(yy, cnt)
+        start = np.repeat(za - np.concatenate(([0], np.cumsum(cnt)[:-1])), cnt)
+        zz = start + np.arange(tot)
+        out.append(np.stack([rep_x, rep_y, zz], 1))
+    if not out:
+        return np.zeros((0, 3), np.int64)
+    return np.concatenate(out, 0)
+
+
+def morton3(x: np.ndarray, y: np.ndarray, z: np.ndarray) -> np.ndarray:
+    """3-D Morton code of non-negative coordinates < 2^21 (x occupies bit 0, y bit 1, z bit 2)."""
+    def spread(v):
+        v = v.astype(np.uint64) & np.uint64(0x1FFFFF)
+        v = (v | (v << np.uint64(32))) & np.uint64(0x1F00000000FFFF)
+        v = (v | (v << np.uint64(16))) & np.uint64(0x1F0000FF0000FF)
+        v = (v | (v << np.uint64(8))) & np.uint64(0x100F00F00F00F00F)
+        v = (v | (v << np.uint64(4))) & np.uint64(0x10C30C30C30C30C3)
+        v = (v | (v << np.uint64(2))) & np.uint64(0x1249249249249249)
+        return v
+    return spread(x) | (spread(y) << np.uint64(1)) | (spread(z) << np.uint64(2))
+
+
+def shell_coords(cfg: Config, grid: int | None = None) -> np.ndarray:
+    """int32 [N,4] (0,x,y,z), unique, Morton-sorted, for the union-shell described by ``cfg``."""
+    g = cfg.grid if grid is None else grid
+    rng = np.random.default_rng(cfg.seed)
+    cen, ax = _shapes(cfg, rng)
+    h = cfg.half_thickness
+    codes = []
+    for i in range(len(cen)):
+        p = _candidates(g, cen[i], ax[i], h)
+        if len(p):
+            codes.append(np.unique(morton3(p[:, 0], p[:, 1], p[:, 2])))
+    if not codes:
+        return np.zeros((0, 4), np.int32)
+    code = np.unique(np.concatenate(codes))
+    p = _unmorton(code)
+    keep = np.zeros(len(p), bool)
+    step = 1 << 21
+    for s in range(0, len(p), step):
+        q = p[s:s + step].astype(np.float64)
+        f = np.full(len(q), np.inf)
+        for i in range(len(cen)):
+            f = np.minimum(f, _f(q, cen[i], ax[i]))
+        keep[s:s + step] = np.abs(f) <= h
+    p = p[keep]
+    out = np.zeros((len(p), 4), np.int32)
+    out[:, 1:] = p
+    return out
+
+
+def _unmorton(code: np.ndarray) -> np.ndarray:
+    def compact(v):
+        v = v & np.uint64(0x1249249249249249)
+        v = (v ^ (v >> np.uint64(2))) & np.uint64(0x10C30C30C30C30C3)
+        v = (v ^ (v >> np.uint64(4))) & np.uint64(0x100F00F00F00F00F)
+        v = (v ^ (v >> np.uint64(8))) & np.uint64(0x1F0000FF0000FF)
+        v = (v ^ (v >> np.uint64(16))) & np.uint64(0x1F00000000FFFF)
+        v = (v ^ (v >> np.uint64(32))) & np.uint64(0x1FFFFF)
+        return v.astype(np.int64)
+    return np.stack([compact(code), compact(code >> np.uint64(1)), compact(code >> np.uint64(2))], 1)
+
+
+def keep_logits(n_parents: int, keep_frac: float, seed: int) -> np.ndarray:
+    """Per-child subdivision logits [n,8] float16: +1 keeps the child (seeded Bernoulli(keep_frac)), -1 drops it.
+
+    The reference's subdivision keeps a child when its fp16 logit is > 0 (``src/sdec.cu:23,30``)."""
+    rng = np.random.default_rng(seed + 77)
+    keep = rng.random((n_parents, 8)) < keep_frac
+    return np.where(keep, 1.0, -1.0).astype(np.float16)
+
+
+def features(n: int, c: int, seed: int, std: float = 1.0) -> np.ndarray:
+    return (np.random.default_rng(seed).standard_normal((n, c), dtype=np.float32) * std).astype(np.float32)
+
+
+def conv_params(cfg: Config, seed: int | None = None, ci: int | None = None, co: int | None = None):
+    """weights [Co,27,Ci] ~ N(0, 1/(27 Ci)), bias [Co] ~ N(0, 0.01) (std 0.1), both fp32."""
+    ci = cfg.ci if ci is None else ci
+    co = cfg.co if co is None else co
+    rng = np.random.default_rng((cfg.seed if seed is None else seed) + 17)
+    w = rng.standard_normal((co, 27, ci), dtype=np.float32) * np.float32(1.0 / np.sqrt(27 * ci))
+    b = rng.standard_normal((co,), dtype=np.float32) * np.float32(0.1)
+    return w.astype(np.float32), b.astype(np.float32)
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """Round fp32 to the nearest bf16 (ties to even) and return the widened fp32 value."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000))
+    nan = np.isnan(a)
+    out = r.view(np.float32).copy()
+    out[nan] = np.nan
+    return out
+
+
+def to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    return (bf16_round(a).view(np.uint32) >> np.uint32(16)).astype(np.uint16)
