@@ -15,6 +15,8 @@
 // The next offset's neighbour indices are fetched one offset ahead so the gather never waits on the nbr load.
 // Workgroups are mapped so each XCD (each L2) walks a contiguous range of tiles with both channel tiles of a row
 // tile adjacent in time.
+#include <utility>
+
 #include "spconv.h"
 
 namespace {
@@ -22,6 +24,8 @@ constexpr uint32_t EMPTY = 0xffffffffu;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte load/store unit (native vector, not a struct)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {  // round to nearest even, quiet NaN preserved
@@ -44,12 +48,16 @@ __device__ __forceinline__ void store_elem(void* p, i64 i, int dt, float v) {
 }
 
 template <bool F16>
-__device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   if constexpr (F16)
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   else
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
+
+// A zero feature row (device .bss): EMPTY neighbours gather from here, so every gather is an unconditional load.
+constexpr int kMaxCi = 8192;
+__device__ __attribute__((aligned(16))) uint16_t kZeroRow[kMaxCi];
 
 struct ConvArgs {
   const uint16_t* x;
@@ -59,6 +67,7 @@ struct ConvArgs {
   void* out;
   const uint32_t* nbr;
   const int32_t* order;
+  const int32_t* gray;
   const uint32_t* code;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
@@ -105,19 +114,19 @@ __global__ void __launch_bounds__(WGM* WGN * 64) k_conv(ConvArgs a) {
   if (nv >= 0) fetch(nv, srcN);
   int kc = 0;
 
-  uint4 ra[AL], rb[BL];
+  u32x4 ra[AL], rb[BL];
   auto gload = [&]() {
     const int k0 = kc * KC;
 #pragma unroll
     for (int j = 0; j < AL; j++) {
       int pc = (tid + j * NT) % PC;
-      ra[j] = srcA[j] == EMPTY ? make_uint4(0, 0, 0, 0)
-                               : *(const uint4*)(a.x + (i64)srcA[j] * Ci + k0 + pc * 8);
+      ra[j] = srcA[j] == EMPTY ? u32x4{0, 0, 0, 0}
+                               : *(const u32x4*)(a.x + (i64)srcA[j] * Ci + k0 + pc * 8);
     }
 #pragma unroll
     for (int j = 0; j < BL; j++) {
       int q = tid + j * NT, r = q / PC, pc = q % PC;
-      rb[j] = *(const uint4*)(a.w + ((i64)(co0 + r) * 27 + cv) * Ci + k0 + pc * 8);
+      rb[j] = *(const u32x4*)(a.w + ((i64)(co0 + r) * 27 + cv) * Ci + k0 + pc * 8);
     }
   };
   auto advance = [&]() {
@@ -135,12 +144,12 @@ __global__ void __launch_bounds__(WGM* WGN * 64) k_conv(ConvArgs a) {
 #pragma unroll
     for (int j = 0; j < AL; j++) {
       int q = tid + j * NT;
-      *(uint4*)&As[buf][(q / PC) * LD + (q % PC) * 8] = ra[j];
+      *(u32x4*)&As[buf][(q / PC) * LD + (q % PC) * 8] = ra[j];
     }
 #pragma unroll
     for (int j = 0; j < BL; j++) {
       int q = tid + j * NT;
-      *(uint4*)&Bs[buf][(q / PC) * LD + (q % PC) * 8] = rb[j];
+      *(u32x4*)&Bs[buf][(q / PC) * LD + (q % PC) * 8] = rb[j];
     }
   };
 
@@ -165,13 +174,13 @@ __global__ void __launch_bounds__(WGM* WGN * 64) k_conv(ConvArgs a) {
     }
 #pragma unroll
     for (int ks = 0; ks < KC / 16; ks++) {
-      uint4 fa[TM], fb[TN];
+      u32x4 fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; i++)
-        fa[i] = *(const uint4*)&As[buf][(wm * WTM + i * 32 + (lane & 31)) * LD + ks * 16 + (lane >> 5) * 8];
+        fa[i] = *(const u32x4*)&As[buf][(wm * WTM + i * 32 + (lane & 31)) * LD + ks * 16 + (lane >> 5) * 8];
 #pragma unroll
       for (int j = 0; j < TN; j++)
-        fb[j] = *(const uint4*)&Bs[buf][(wn * WTN + j * 32 + (lane & 31)) * LD + ks * 16 + (lane >> 5) * 8];
+        fb[j] = *(const u32x4*)&Bs[buf][(wn * WTN + j * 32 + (lane & 31)) * LD + ks * 16 + (lane >> 5) * 8];
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -203,6 +212,259 @@ __global__ void __launch_bounds__(WGM* WGN * 64) k_conv(ConvArgs a) {
   }
 }
 
+// Compile-time unrolled loop: f(std::integral_constant<int, i>) for i in [0, N) (keeps register arrays indexed by
+// constants, so they never fall back to scratch memory).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+__device__ __forceinline__ float silu(float v) { return v * __frcp_rn(1.0f + __expf(-v)); }
+
+// Epilogue of one 32-row x 64-channel accumulator group, staged through LDS so every lane writes 16 contiguous
+// bytes: out[order[r], co] = act(acc + b) [+ residual]. `ew` is this wavefront's private [32][72] fp32 area.
+template <int TN>
+__device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TN], float* ew, const int* tile_order, int rbase,
+                                               int nrows, int co_w, const float (&bias8)[8], const ConvArgs& a,
+                                               int lane) {
+  constexpr int ES = 72;  // row stride in floats: 4 rows apart differ by 32 banks, so the scatter is conflict-free
+  const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int t = 0; t < TN; t++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) ew[((e >> 2) * 8 + h * 4 + (e & 3)) * ES + t * 32 + l32] = acc[t][e];
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+  const int c8 = (lane & 7) * 8;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const int rr = p * 8 + (lane >> 3);
+    if (rbase + rr >= nrows) continue;
+    const i64 o = (i64)tile_order[rbase + rr] * a.Co + co_w + c8;
+    float v[8];
+    *(f32x4*)&v[0] = *(const f32x4*)&ew[rr * ES + c8];
+    *(f32x4*)&v[4] = *(const f32x4*)&ew[rr * ES + c8 + 4];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      v[q] += bias8[q];
+      if (a.act == ACT_SILU) v[q] = silu(v[q]);
+    }
+    if (a.res) {
+      if (a.res_dt == F32) {
+        f32x4 r0 = *(const f32x4*)((const float*)a.res + o), r1 = *(const f32x4*)((const float*)a.res + o + 4);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          v[q] += r0[q];
+          v[q + 4] += r1[q];
+        }
+      } else {
+        u32x4 r = *(const u32x4*)((const uint16_t*)a.res + o);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          uint16_t hv = (uint16_t)(r[q >> 1] >> ((q & 1) * 16));
+          v[q] += a.res_dt == BF16 ? bf16_to_f32(hv) : f16_to_f32(hv);
+        }
+      }
+    }
+    if (a.out_dt == F32) {
+      *(f32x4*)((float*)a.out + o) = f32x4{v[0], v[1], v[2], v[3]};
+      *(f32x4*)((float*)a.out + o + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    } else {
+      u32x4 w;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        uint32_t lo = a.out_dt == BF16 ? f32_to_bf16(v[2 * q]) : f32_to_f16(v[2 * q]);
+        uint32_t hi = a.out_dt == BF16 ? f32_to_bf16(v[2 * q + 1]) : f32_to_f16(v[2 * q + 1]);
+        w[q] = lo | (hi << 16);
+      }
+      *(u32x4*)((uint16_t*)a.out + o) = w;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Wide-channel kernel: BM sorted rows x BN = 64*NW channels, NW wavefronts; each wavefront owns all BM rows x its
+// own 64 channels (BM/32 x 2 tiles of 32x32 fp32 accumulators).
+//  * Traffic: per K stage (one offset v x 64 input channels) a workgroup reads BM gathered rows and BN weight rows
+//    of 128 bytes, for 2*BM*BN*64 flops; BM = BN = 256 keeps this at 0.0078 byte/flop, which L2 can feed.
+//  * Skipping: the K loop runs over the union of the tile's neighbour masks, but each 32-row group has its own
+//    mask and skips its MFMAs for offsets none of its rows has, so padding work follows 32-row granularity.
+//  * Software pipeline: stage s issues the gather loads of A(s+2) and the weight loads of B(s+1), runs the MFMAs of
+//    stage s (A(s) from LDS, B(s) from registers), then writes A(s+1) -- loaded a full stage earlier -- into the
+//    other LDS buffer and synchronises. The loop is unrolled by two so registers and buffers have fixed names.
+//  * Only A is shared by the wavefronts, so only A goes through LDS; weights (L2-resident) stream straight into
+//    MFMA operand registers. At tile start the offset list, the 32-row masks, the tile's output row indices and its
+//    [BM x 27] neighbour indices are staged in LDS: the K loop has no dependent global loads. EMPTY neighbours
+//    gather from a zero row in device memory, so every gather is an unconditional 16-byte load.
+//  * LDS layout of a stage: row r occupies 128 contiguous bytes as eight 16-byte slots; channel piece p of row r is
+//    stored in slot p ^ (r & 7) so the MFMA operand reads (32 rows, one piece) hit distinct banks.
+//  * Within a 64-channel stage the K order is permuted (lane half h, step j -> piece h*4 + j) identically for A and
+//    B, so each lane's four weight loads are one contiguous 64-byte run.
+//  * Epilogue: per 32-row group, accumulators go through LDS and leave as 16-byte row segments (bias, SiLU,
+//    residual fused, one rounding).
+template <bool F16, int NW, int BM>
+__global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
+  constexpr int NT = NW * 64, KC = 64, PC = KC / 8;
+  constexpr int TM = BM / 32, TN = 2, AL = BM * PC / NT;  // AL gather loads per lane per stage
+  static_assert(AL * NT == BM * PC && TM <= 8, "tile shape");
+  __shared__ __attribute__((aligned(16))) u32x4 As[2][BM * PC];
+  __shared__ uint32_t srcT[BM * 27];
+  __shared__ int ordT[BM];
+  __shared__ uint32_t gmask[TM];
+  __shared__ int vlist[32];
+
+  const int g = blockIdx.x, per = a.grid / 8;
+  const int logical = (g % 8) * per + g / 8;
+  if (logical >= a.tiles_m * a.tiles_n) return;
+  const int tm_ = logical / a.tiles_n, tn_ = logical % a.tiles_n;
+  const int row0 = tm_ * BM, co0 = tn_ * (64 * NW);
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31, wn = tid >> 6;
+  const int N = a.N, Ci = a.Ci, nkc = Ci / KC;
+
+  // prologue: row indices, 32-row masks (OR of the rows' neighbour masks), offset list, neighbour table
+  for (int r = tid; r < BM; r += NT) {
+    const int row = row0 + r;
+    const int o = row < N ? a.order[row] : 0;
+    ordT[r] = o;
+    uint32_t gm = row < N ? (uint32_t)a.gray[o] : 0u;
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
+    if ((r & 31) == 0) gmask[r >> 5] = gm;
+  }
+  __syncthreads();
+  uint32_t mask = 0;
+#pragma unroll
+  for (int i = 0; i < TM; i++) mask |= gmask[i];
+  const int nvv = __popc(mask), total = nvv * nkc;
+  if (tid < 27 && ((mask >> tid) & 1u)) vlist[__popc(mask & ((1u << tid) - 1u))] = tid;
+  for (int i = tid; i < BM * 27; i += NT) {
+    const int r = i / 27, v = i - r * 27;
+    srcT[i] = row0 + r < N ? a.nbr[(i64)ordT[r] * 27 + v] : EMPTY;
+  }
+  uint32_t gms[TM];
+#pragma unroll
+  for (int i = 0; i < TM; i++) gms[i] = __builtin_amdgcn_readfirstlane(gmask[i]);
+  __syncthreads();
+
+  // this lane's gather pieces: LDS unit u = k*NT + tid -> row u/8, slot u%8, channel piece slot ^ (row & 7)
+  int arow[AL], apiece[AL];
+#pragma unroll
+  for (int k = 0; k < AL; k++) {
+    int u = k * NT + tid;
+    arow[k] = u >> 3;
+    apiece[k] = (u & 7) ^ (arow[k] & 7);
+  }
+  const uint16_t* wrow[TN];
+#pragma unroll
+  for (int t = 0; t < TN; t++) wrow[t] = a.w + (i64)(co0 + wn * 64 + t * 32 + l32) * 27 * Ci + h * 32;
+
+  // stage cursors (offset index, channel block); loads past the last stage re-read the last stage
+  int avi = 0, akc = 0, bvi = 0, bkc = 0, cvi = 0, ckc = 0;
+  auto next = [&](int& vi, int& kc) __attribute__((always_inline)) {
+    const bool wrap = kc + 1 == nkc;
+    kc = wrap ? 0 : kc + 1;
+    vi += wrap ? 1 : 0;
+  };
+  auto load_a = [&](u32x4 (&ra)[AL]) __attribute__((always_inline)) {
+    const bool live = avi < nvv;
+    const int v = vlist[live ? avi : nvv - 1], k0 = (live ? akc : nkc - 1) * KC;
+#pragma unroll
+    for (int k = 0; k < AL; k++) {
+      uint32_t src = srcT[arow[k] * 27 + v];
+      const uint16_t* rowp = src == EMPTY ? kZeroRow : a.x + (i64)src * Ci;
+      ra[k] = *(const u32x4*)(rowp + k0 + apiece[k] * 8);
+    }
+    next(avi, akc);
+  };
+  auto store_a = [&](int buf, const u32x4 (&ra)[AL]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < AL; k++) As[buf][k * NT + tid] = ra[k];
+  };
+  auto load_b = [&](u32x4 (&rb)[TN][4]) __attribute__((always_inline)) {
+    const bool live = bvi < nvv;
+    const int v = vlist[live ? bvi : nvv - 1], k0 = (live ? bkc : nkc - 1) * KC;
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+      const u32x4* p = (const u32x4*)(wrow[t] + (i64)v * Ci + k0);
+#pragma unroll
+      for (int j = 0; j < 4; j++) rb[t][j] = p[j];
+    }
+    next(bvi, bkc);
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int t = 0; t < TN; t++) acc[i][t] = f32x16{};
+  auto compute = [&](int buf, const u32x4 (&rb)[TN][4]) __attribute__((always_inline)) {
+    const uint32_t vbit = 1u << __builtin_amdgcn_readfirstlane(vlist[cvi]);
+    next(cvi, ckc);
+    u32x4 fa[2][4];
+    auto read_fa = [&](u32x4 (&f)[4], int i) __attribute__((always_inline)) {
+      const int r = i * 32 + l32;
+#pragma unroll
+      for (int j = 0; j < 4; j++) f[j] = As[buf][r * PC + ((h * 4 + j) ^ (r & 7))];
+    };
+    read_fa(fa[0], 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      if (i + 1 < TM) read_fa(fa[(i + 1) & 1], i + 1);
+      if (gms[i] & vbit) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int t = 0; t < TN; t++) acc[i][t] = mfma32<F16>(fa[i & 1][j], rb[t][j], acc[i][t]);
+      }
+    }
+  };
+
+  if (total > 0) {
+    u32x4 ra0[AL], ra1[AL], rb0[TN][4], rb1[TN][4];
+    load_a(ra0);  // A(0)
+    load_b(rb0);  // B(0)
+    load_a(ra1);  // A(1)
+    store_a(0, ra0);
+    __syncthreads();
+    for (int s = 0; s < total; s += 2) {
+      load_a(ra0);  // A(s+2)
+      load_b(rb1);  // B(s+1)
+      compute(0, rb0);
+      store_a(1, ra1);  // A(s+1)
+      __syncthreads();
+      load_a(ra1);  // A(s+3)
+      load_b(rb0);  // B(s+2)
+      if (s + 1 < total) compute(1, rb1);
+      store_a(0, ra0);  // A(s+2)
+      __syncthreads();
+    }
+  }
+
+  // epilogue through this wavefront's share of the (now idle) A buffers
+  float* ew = (float*)&As[0][0] + wn * (32 * 72);
+  static_assert(NW * 32 * 72 * 4 <= 2 * BM * PC * 16, "epilogue staging fits in the A buffers");
+  const int co_w = co0 + wn * 64;
+  float bias8[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[co_w + (lane & 7) * 8 + q] : 0.f;
+  const int nrows = N - row0;
+  static_for<TM>([&](auto I) { epilogue_group<TN>(acc[I], ew, ordT, I * 32, nrows, co_w, bias8, a, lane); });
+}
+
+template <bool F16, int NW, int BM>
+void launch_wide(ConvArgs a) {
+  a.tiles_m = cdiv(a.N, BM);
+  a.tiles_n = a.Co / (64 * NW);
+  int tiles = a.tiles_m * a.tiles_n;
+  a.grid = (tiles + 7) / 8 * 8;
+  k_conv_wide<F16, NW, BM><<<a.grid, NW * 64, 0, stream()>>>(a);
+}
+
 __global__ void k_to_f32(const void* p, int dt, int n, float* o) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) o[i] = load_elem(p, i, dt);
@@ -220,6 +482,8 @@ void launch(ConvArgs a) {
 template <bool F16>
 void dispatch(const SpConvCfg& cfg, ConvArgs a) {
   // Fixed tiles per channel width (no autotune): BM = 128 sorted rows per tile.
+  if (cfg.BK == 64 && a.Co % 256 == 0) return launch_wide<F16, 4, 256>(a);
+  if (cfg.BK == 64 && a.Co % 128 == 0) return launch_wide<F16, 2, 128>(a);
   if (a.Co % 128 == 0) {
     if (cfg.BK == 64) launch<F16, 128, 128, 2, 2, 64>(a);
     else launch<F16, 128, 128, 2, 2, 32>(a);
@@ -243,7 +507,7 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   REQ((x.dt == BF16 || x.dt == F16) && w.dt == x.dt, "x and w must both be bf16 or both fp16 (x %s, w %s)",
       dname(x.dt), dname(w.dt));
   REQ(w.size(1) == 27 && w.size(2) == Ci, "w must be [Co,27,%d]", Ci);
-  REQ(Ci > 0 && Ci % 32 == 0, "Ci=%d must be a multiple of 32", Ci);
+  REQ(Ci > 0 && Ci % 32 == 0 && Ci <= kMaxCi, "Ci=%d must be a multiple of 32 (at most %d)", Ci, kMaxCi);
   REQ(Co > 0 && Co % 64 == 0, "Co=%d must be a multiple of 64", Co);
   REQ(N == c.N, "x has %d rows, neighbour cache %d", N, c.N);
   REQ(act == ACT_NONE || act == ACT_SILU, "act=%d", act);
@@ -276,6 +540,7 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   a.out_dt = out.dt;
   a.nbr = c.nbr.ptr<uint32_t>();
   a.order = c.sorted.ptr<int32_t>();
+  a.gray = c.gray.ptr<int32_t>();
   a.code = code.ptr<uint32_t>();
   a.N = N;
   a.Ci = Ci;
