@@ -59,6 +59,16 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 constexpr int kMaxCi = 8192;
 __device__ __attribute__((aligned(16))) uint16_t kZeroRow[kMaxCi];
 
+// Offset used for an EMPTY neighbour: past the end of any gathered buffer (sizes are checked to stay below it),
+// so the buffer load's range check returns zeros.
+constexpr uint32_t kOutOfRange = 0xffff0000u;
+constexpr uint64_t kMaxBufferBytes = 0xfffe0000ull;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  // word 3 = 0x00020000: 32-bit data format, the raw-buffer setting for gfx9-family (CDNA) parts
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+
 struct ConvArgs {
   const uint16_t* x;
   const uint16_t* w;
@@ -71,6 +81,7 @@ struct ConvArgs {
   const uint32_t* code;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
+  uint32_t x_bytes, w_bytes;
 };
 
 template <bool F16, int BM, int BN, int WGM, int WGN, int KC>
@@ -342,9 +353,16 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
   for (int i = 0; i < TM; i++) mask |= gmask[i];
   const int nvv = __popc(mask), total = nvv * nkc;
   if (tid < 27 && ((mask >> tid) & 1u)) vlist[__popc(mask & ((1u << tid) - 1u))] = tid;
-  for (int i = tid; i < BM * 27; i += NT) {
-    const int r = i / 27, v = i - r * 27;
-    srcT[i] = row0 + r < N ? a.nbr[(i64)ordT[r] * 27 + v] : EMPTY;
+  const uint32_t row_bytes = (uint32_t)Ci * 2u;
+  // one row per thread: its 27 neighbour indices are one contiguous 108-byte run, loaded as 27 independent loads
+  for (int r = tid; r < BM; r += NT) {
+    uint32_t src[27];
+    const bool live = row0 + r < N;
+    const uint32_t* nrow = a.nbr + (i64)ordT[r] * 27;
+#pragma unroll
+    for (int v = 0; v < 27; v++) src[v] = live ? nrow[v] : EMPTY;
+#pragma unroll
+    for (int v = 0; v < 27; v++) srcT[r * 27 + v] = src[v] == EMPTY ? kOutOfRange : src[v] * row_bytes;
   }
   uint32_t gms[TM];
 #pragma unroll
@@ -359,9 +377,12 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
     arow[k] = u >> 3;
     apiece[k] = (u & 7) ^ (arow[k] & 7);
   }
-  const uint16_t* wrow[TN];
-#pragma unroll
-  for (int t = 0; t < TN; t++) wrow[t] = a.w + (i64)(co0 + wn * 64 + t * 32 + l32) * 27 * Ci + h * 32;
+  // buffer resources: 32-bit offsets, and gathers of EMPTY neighbours (offset kOutOfRange) return zeros
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes), rw = make_rsrc(a.w, a.w_bytes);
+  // packed weights: the stage (v, kc) fragment of this wavefront's 64-channel slice is 8 KiB at
+  // ((slice*27 + v)*nkc + kc) * 8 KiB, as [t][j][lane][16 bytes]
+  const uint32_t wslice = (uint32_t)((co0 >> 6) + wn) * 27u * (uint32_t)nkc;
+  const uint32_t wlane = (uint32_t)lane * 16u;
 
   // stage cursors (offset index, channel block); loads past the last stage re-read the last stage
   int avi = 0, akc = 0, bvi = 0, bkc = 0, cvi = 0, ckc = 0;
@@ -372,13 +393,14 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
   };
   auto load_a = [&](u32x4 (&ra)[AL]) __attribute__((always_inline)) {
     const bool live = avi < nvv;
-    const int v = vlist[live ? avi : nvv - 1], k0 = (live ? akc : nkc - 1) * KC;
+    const int v = __builtin_amdgcn_readfirstlane(vlist[live ? avi : nvv - 1]);
+    const int k0 = __builtin_amdgcn_readfirstlane((live ? akc : nkc - 1) * KC);
+    uint32_t off[AL];
 #pragma unroll
-    for (int k = 0; k < AL; k++) {
-      uint32_t src = srcT[arow[k] * 27 + v];
-      const uint16_t* rowp = src == EMPTY ? kZeroRow : a.x + (i64)src * Ci;
-      ra[k] = *(const u32x4*)(rowp + k0 + apiece[k] * 8);
-    }
+    for (int k = 0; k < AL; k++) off[k] = srcT[arow[k] * 27 + v];
+#pragma unroll
+    for (int k = 0; k < AL; k++)
+      ra[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, off[k] + apiece[k] * 16, k0 * 2, 0);
     next(avi, akc);
   };
   auto store_a = [&](int buf, const u32x4 (&ra)[AL]) __attribute__((always_inline)) {
@@ -387,13 +409,13 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
   };
   auto load_b = [&](u32x4 (&rb)[TN][4]) __attribute__((always_inline)) {
     const bool live = bvi < nvv;
-    const int v = vlist[live ? bvi : nvv - 1], k0 = (live ? bkc : nkc - 1) * KC;
+    const int v = __builtin_amdgcn_readfirstlane(vlist[live ? bvi : nvv - 1]);
+    const int k0 = __builtin_amdgcn_readfirstlane((live ? bkc : nkc - 1) * KC);
+    const int soff = __builtin_amdgcn_readfirstlane((int)((wslice + (uint32_t)(v * nkc) + (uint32_t)(k0 / KC)) * 8192u));
 #pragma unroll
-    for (int t = 0; t < TN; t++) {
-      const u32x4* p = (const u32x4*)(wrow[t] + (i64)v * Ci + k0);
+    for (int t = 0; t < TN; t++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) rb[t][j] = p[j];
-    }
+      for (int j = 0; j < 4; j++) rb[t][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + (t * 4 + j) * 1024, soff, 0);
     next(bvi, bkc);
   };
 
@@ -463,6 +485,29 @@ void launch_wide(ConvArgs a) {
   int tiles = a.tiles_m * a.tiles_n;
   a.grid = (tiles + 7) / 8 * 8;
   k_conv_wide<F16, NW, BM><<<a.grid, NW * 64, 0, stream()>>>(a);
+}
+
+// Weight repack for the wide kernel: w [Co,27,Ci] -> one 1 KiB block per (64-channel output slice, offset v,
+// 64-channel input block kc, 32-column half t, step j), laid out as 64 lanes x 16 bytes in MFMA operand order:
+// lane l holds column c = slice*64 + t*32 + (l & 31), input channels kc*64 + (l >> 5)*32 + j*8 .. +8.
+// A wavefront then fetches a stage's weight fragment with fully coalesced 1 KiB loads.
+__global__ void k_pack_w(const u32x4* __restrict__ w, u32x4* __restrict__ wp, int Co, int Ci) {
+  const i64 q = (i64)blockIdx.x * blockDim.x + threadIdx.x;  // destination 16-byte chunk
+  const int nkc = Ci / 64;
+  const i64 total = (i64)Co * 27 * Ci / 8;
+  if (q >= total) return;
+  const int lane = (int)(q & 63);
+  i64 r = q >> 6;
+  const int j = (int)(r & 3);
+  r >>= 2;
+  const int t = (int)(r & 1);
+  r >>= 1;
+  const int kc = (int)(r % nkc);
+  r /= nkc;
+  const int v = (int)(r % 27);
+  const int slice = (int)(r / 27);
+  const int co = slice * 64 + t * 32 + (lane & 31), ch = kc * 64 + (lane >> 5) * 32 + j * 8;
+  wp[q] = w[((i64)co * 27 + v) * Ci / 8 + ch / 8];
 }
 
 __global__ void k_to_f32(const void* p, int dt, int n, float* o) {
@@ -542,10 +587,21 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   a.order = c.sorted.ptr<int32_t>();
   a.gray = c.gray.ptr<int32_t>();
   a.code = code.ptr<uint32_t>();
+  REQ((uint64_t)N * Ci * 2 <= kMaxBufferBytes && (uint64_t)Co * 27 * Ci * 2 <= kMaxBufferBytes,
+      "x or w larger than %llu bytes", (unsigned long long)kMaxBufferBytes);
+  a.x_bytes = (uint32_t)((uint64_t)N * Ci * 2);
+  a.w_bytes = (uint32_t)((uint64_t)Co * 27 * Ci * 2);
   a.N = N;
   a.Ci = Ci;
   a.Co = Co;
   a.act = act;
+  Tensor wpack;
+  if (cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the MFMA-ordered weight copy
+    wpack = empty({(i64)Co * 27 * Ci}, x.dt);
+    i64 chunks = (i64)Co * 27 * Ci / 8;
+    k_pack_w<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
+    a.w = wpack.ptr<uint16_t>();
+  }
   if (x.dt == F16) dispatch<true>(cfg, a);
   else dispatch<false>(cfg, a);
   CK(hipGetLastError());
