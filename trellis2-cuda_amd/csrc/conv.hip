@@ -424,9 +424,29 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
   for (int i = 0; i < TM; i++)
 #pragma unroll
     for (int t = 0; t < TN; t++) acc[i][t] = f32x16{};
-  auto compute = [&](int buf, const u32x4 (&rb)[TN][4]) __attribute__((always_inline)) {
+  // One K stage, with the next stages' traffic interleaved between the MFMA groups so the vector-memory and LDS
+  // queues drain while the matrix cores run: group i issues its share of the A(s+2) gathers and B(s+1) weight
+  // loads, writes its share of A(s+1) (loaded a stage ago) into the other LDS buffer, prefetches the operands of
+  // group i+1, then runs its MFMAs if any of its 32 rows has offset v.
+  auto stage = [&](int buf, const u32x4 (&rbC)[TN][4], const u32x4 (&raW)[AL], u32x4 (&raL)[AL],
+                   u32x4 (&rbN)[TN][4]) __attribute__((always_inline)) {
     const uint32_t vbit = 1u << __builtin_amdgcn_readfirstlane(vlist[cvi]);
     next(cvi, ckc);
+    // A(s+2) addresses
+    const bool alive = avi < nvv;
+    const int va = __builtin_amdgcn_readfirstlane(vlist[alive ? avi : nvv - 1]);
+    const int ka = __builtin_amdgcn_readfirstlane((alive ? akc : nkc - 1) * KC * 2);
+    next(avi, akc);
+    uint32_t off[AL];
+#pragma unroll
+    for (int k = 0; k < AL; k++) off[k] = srcT[arow[k] * 27 + va] + apiece[k] * 16;
+    // B(s+1) base
+    const bool blive = bvi < nvv;
+    const int vb = __builtin_amdgcn_readfirstlane(vlist[blive ? bvi : nvv - 1]);
+    const int kb = blive ? bkc : nkc - 1;
+    const int soff = __builtin_amdgcn_readfirstlane((int)((wslice + (uint32_t)(vb * nkc + kb)) * 8192u));
+    next(bvi, bkc);
+
     u32x4 fa[2][4];
     auto read_fa = [&](u32x4 (&f)[4], int i) __attribute__((always_inline)) {
       const int r = i * 32 + l32;
@@ -434,16 +454,26 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
       for (int j = 0; j < 4; j++) f[j] = As[buf][r * PC + ((h * 4 + j) ^ (r & 7))];
     };
     read_fa(fa[0], 0);
+    constexpr int AG = AL / TM, BG = TN * 4 / TM;  // loads per group
+    static_assert(AG * TM == AL && BG * TM == TN * 4 && BG >= 1, "load split");
 #pragma unroll
     for (int i = 0; i < TM; i++) {
+#pragma unroll
+      for (int k = i * AG; k < (i + 1) * AG; k++) raL[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, off[k], ka, 0);
+#pragma unroll
+      for (int q = i * BG; q < (i + 1) * BG; q++)
+        rbN[q / 4][q % 4] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + q * 1024, soff, 0);
+#pragma unroll
+      for (int k = i * AG; k < (i + 1) * AG; k++) As[buf ^ 1][k * NT + tid] = raW[k];
       if (i + 1 < TM) read_fa(fa[(i + 1) & 1], i + 1);
       if (gms[i] & vbit) {
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
-          for (int t = 0; t < TN; t++) acc[i][t] = mfma32<F16>(fa[i & 1][j], rb[t][j], acc[i][t]);
+          for (int t = 0; t < TN; t++) acc[i][t] = mfma32<F16>(fa[i & 1][j], rbC[t][j], acc[i][t]);
       }
     }
+    __syncthreads();
   };
 
   if (total > 0) {
@@ -454,16 +484,9 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
     store_a(0, ra0);
     __syncthreads();
     for (int s = 0; s < total; s += 2) {
-      load_a(ra0);  // A(s+2)
-      load_b(rb1);  // B(s+1)
-      compute(0, rb0);
-      store_a(1, ra1);  // A(s+1)
-      __syncthreads();
-      load_a(ra1);  // A(s+3)
-      load_b(rb0);  // B(s+2)
-      if (s + 1 < total) compute(1, rb1);
-      store_a(0, ra0);  // A(s+2)
-      __syncthreads();
+      stage(0, rb0, ra1, ra0, rb1);  // MFMAs of stage s; writes A(s+1); loads A(s+2), B(s+1)
+      if (s + 1 >= total) break;
+      stage(1, rb1, ra0, ra1, rb0);  // stage s+1; writes A(s+2); loads A(s+3), B(s+2)
     }
   }
 
