@@ -375,7 +375,7 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
   for (int k = 0; k < AL; k++) {
     int u = k * NT + tid;
     arow[k] = u >> 3;
-    apiece[k] = (u & 7) ^ (arow[k] & 7);
+    apiece[k] = (u & 7) ^ ((arow[k] >> 1) & 7);
   }
   // buffer resources: 32-bit offsets, and gathers of EMPTY neighbours (offset kOutOfRange) return zeros
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes), rw = make_rsrc(a.w, a.w_bytes);
@@ -451,7 +451,7 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
     auto read_fa = [&](u32x4 (&f)[4], int i) __attribute__((always_inline)) {
       const int r = i * 32 + l32;
 #pragma unroll
-      for (int j = 0; j < 4; j++) f[j] = As[buf][r * PC + ((h * 4 + j) ^ (r & 7))];
+      for (int j = 0; j < 4; j++) f[j] = As[buf][r * PC + ((h * 4 + j) ^ ((r >> 1) & 7))];
     };
     read_fa(fa[0], 0);
     constexpr int AG = AL / TM, BG = TN * 4 / TM;  // loads per group
