@@ -87,7 +87,7 @@ def shell(r, h=1.0, grid=None, seed=7):
     return W.shell_coords(W.Config("s", g, 1, (r, r), False, h, 0, 0, "", "", seed, centred=True))
 
 
-@pytest.mark.parametrize("ci,co", [(32, 64), (64, 64), (128, 64), (64, 128), (96, 128), (256, 256), (128, 192)])
+@pytest.mark.parametrize("ci,co", [(32, 64), (64, 64), (96, 64), (128, 64), (64, 128), (96, 128), (256, 256), (128, 192), (256, 512)])
 def test_widths(gpu, ci, co):
     run_case(gpu, shell(9.0), ci, co, out_dt="bf16")
 

@@ -236,6 +236,83 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 __device__ __forceinline__ float silu(float v) { return v * __frcp_rn(1.0f + __expf(-v)); }
 
+// bias, activation, residual and one rounding for 8 consecutive output channels at element offset o
+__device__ __forceinline__ void store_row8(const ConvArgs& a, i64 o, float (&v)[8], const float (&bias8)[8]) {
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    v[q] += bias8[q];
+    if (a.act == ACT_SILU) v[q] = silu(v[q]);
+  }
+  if (a.res) {
+    if (a.res_dt == F32) {
+      f32x4 r0 = *(const f32x4*)((const float*)a.res + o), r1 = *(const f32x4*)((const float*)a.res + o + 4);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        v[q] += r0[q];
+        v[q + 4] += r1[q];
+      }
+    } else {
+      u32x4 r = *(const u32x4*)((const uint16_t*)a.res + o);
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        uint16_t hv = (uint16_t)(r[q >> 1] >> ((q & 1) * 16));
+        v[q] += a.res_dt == BF16 ? bf16_to_f32(hv) : f16_to_f32(hv);
+      }
+    }
+  }
+  if (a.out_dt == F32) {
+    *(f32x4*)((float*)a.out + o) = f32x4{v[0], v[1], v[2], v[3]};
+    *(f32x4*)((float*)a.out + o + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  } else {
+    u32x4 w;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint32_t lo = a.out_dt == BF16 ? f32_to_bf16(v[2 * q]) : f32_to_f16(v[2 * q]);
+      uint32_t hi = a.out_dt == BF16 ? f32_to_bf16(v[2 * q + 1]) : f32_to_f16(v[2 * q + 1]);
+      w[q] = lo | (hi << 16);
+    }
+    *(u32x4*)((uint16_t*)a.out + o) = w;
+  }
+}
+
+// store_row8 with the residual segment already loaded (raw bits: 8 x bf16/f16 in r[0], or 8 x f32 in r[0..1])
+__device__ __forceinline__ void store_row8_pre(const ConvArgs& a, i64 o, float (&v)[8], const float (&bias8)[8],
+                                               const u32x4 (&r)[2]) {
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    v[q] += bias8[q];
+    if (a.act == ACT_SILU) v[q] = silu(v[q]);
+  }
+  if (a.res) {
+    if (a.res_dt == F32) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        v[q] += __uint_as_float(r[0][q]);
+        v[q + 4] += __uint_as_float(r[1][q]);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        uint16_t hv = (uint16_t)(r[0][q >> 1] >> ((q & 1) * 16));
+        v[q] += a.res_dt == BF16 ? bf16_to_f32(hv) : f16_to_f32(hv);
+      }
+    }
+  }
+  if (a.out_dt == F32) {
+    *(f32x4*)((float*)a.out + o) = f32x4{v[0], v[1], v[2], v[3]};
+    *(f32x4*)((float*)a.out + o + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  } else {
+    u32x4 w;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint32_t lo = a.out_dt == BF16 ? f32_to_bf16(v[2 * q]) : f32_to_f16(v[2 * q]);
+      uint32_t hi = a.out_dt == BF16 ? f32_to_bf16(v[2 * q + 1]) : f32_to_f16(v[2 * q + 1]);
+      w[q] = lo | (hi << 16);
+    }
+    *(u32x4*)((uint16_t*)a.out + o) = w;
+  }
+}
+
 // Epilogue of one 32-row x 64-channel accumulator group, staged through LDS so every lane writes 16 contiguous
 // bytes: out[order[r], co] = act(acc + b) [+ residual]. `ew` is this wavefront's private [32][72] fp32 area.
 template <int TN>
@@ -259,41 +336,7 @@ __device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TN], float* e
     float v[8];
     *(f32x4*)&v[0] = *(const f32x4*)&ew[rr * ES + c8];
     *(f32x4*)&v[4] = *(const f32x4*)&ew[rr * ES + c8 + 4];
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-      v[q] += bias8[q];
-      if (a.act == ACT_SILU) v[q] = silu(v[q]);
-    }
-    if (a.res) {
-      if (a.res_dt == F32) {
-        f32x4 r0 = *(const f32x4*)((const float*)a.res + o), r1 = *(const f32x4*)((const float*)a.res + o + 4);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          v[q] += r0[q];
-          v[q + 4] += r1[q];
-        }
-      } else {
-        u32x4 r = *(const u32x4*)((const uint16_t*)a.res + o);
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-          uint16_t hv = (uint16_t)(r[q >> 1] >> ((q & 1) * 16));
-          v[q] += a.res_dt == BF16 ? bf16_to_f32(hv) : f16_to_f32(hv);
-        }
-      }
-    }
-    if (a.out_dt == F32) {
-      *(f32x4*)((float*)a.out + o) = f32x4{v[0], v[1], v[2], v[3]};
-      *(f32x4*)((float*)a.out + o + 4) = f32x4{v[4], v[5], v[6], v[7]};
-    } else {
-      u32x4 w;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        uint32_t lo = a.out_dt == BF16 ? f32_to_bf16(v[2 * q]) : f32_to_f16(v[2 * q]);
-        uint32_t hi = a.out_dt == BF16 ? f32_to_bf16(v[2 * q + 1]) : f32_to_f16(v[2 * q + 1]);
-        w[q] = lo | (hi << 16);
-      }
-      *(u32x4*)((uint16_t*)a.out + o) = w;
-    }
+    store_row8(a, o, v, bias8);
   }
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
@@ -501,6 +544,217 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
   static_for<TM>([&](auto I) { epilogue_group<TN>(acc[I], ew, ordT, I * 32, nrows, co_w, bias8, a, lane); });
 }
 
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+template <bool F16>
+__device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Weight repack for the narrow kernel: w [Co,27,Ci] -> per offset v, per 16-column tile t, per 32-channel step m,
+// one 1 KiB block of 64 lanes x 16 bytes in v_mfma_f32_16x16x32 operand order: lane l holds column t*16 + (l & 15),
+// input channels ((l >> 4)*S + m)*8 .. +8 (S = Ci/32 steps; lane quarter q owns channels q*8S .. q*8S + 8S).
+__global__ void k_pack_w_narrow(const u32x4* __restrict__ w, u32x4* __restrict__ wp, int Co, int Ci) {
+  const i64 q = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  const int S = Ci / 32, T = Co / 16;
+  const i64 total = (i64)Co * 27 * Ci / 8;
+  if (q >= total) return;
+  const int lane = (int)(q & 63);
+  i64 r = q >> 6;
+  const int m = (int)(r % S);
+  r /= S;
+  const int t = (int)(r % T);
+  const int v = (int)(r / T);
+  const int co = t * 16 + (lane & 15), ch = ((lane >> 4) * S + m) * 8;
+  wp[q] = w[((i64)co * 27 + v) * Ci / 8 + ch / 8];
+}
+
+// Narrow-channel kernel (Co = 16*T <= 64, Ci = 32*S <= 128): the layers that are bound by HBM traffic (gathers,
+// neighbour table, residual, output) rather than by the matrix cores.
+//  * Workgroup = 4 wavefronts x 64 rows (256 rows of the row order); each wavefront owns its 64 rows x all Co
+//    columns as 4 groups of 16 rows x T tiles of 16x16 fp32 accumulators (v_mfma_f32_16x16x32).
+//  * Gathers go straight from global memory into MFMA operand registers: lane (row r, quarter q) of a 16-row group
+//    loads channels q*8S .. q*8S+8S of the neighbour row (S contiguous 16-byte loads; a row's four lanes read one
+//    contiguous Ci*2-byte run), through a buffer resource whose range check turns EMPTY into zeros.
+//  * Weights: per offset, the [Co x Ci] slice (in MFMA operand order) is staged once per workgroup in LDS
+//    (double-buffered, loaded while the previous offset computes) and shared by the 4 wavefronts.
+//  * Skipping: each 16-row group has its own neighbour mask; groups without offset v issue neither gathers nor
+//    MFMAs for it. Rows come in the order the caller chooses (null = identity); the spatial (Morton) order keeps
+//    the gathers of neighbouring rows in L2.
+//  * Epilogue: per 16-row group, accumulators go through LDS and leave as 16-byte segments of whole output rows.
+template <bool F16, int S, int T>
+__global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
+  constexpr int BM = 256, NT = 256, G = 4, CI = 32 * S, CO = 16 * T, WB = T * S * 64;  // WB: 16B units per offset
+  static_assert(WB % NT == 0, "weight slice split");
+  __shared__ __attribute__((aligned(16))) u32x4 Bs[2][WB];
+  __shared__ __attribute__((aligned(16))) uint32_t srcT[BM * 27];
+  __shared__ int ordT[BM];
+  __shared__ uint32_t gmask[BM / 16];
+  __shared__ int vlist[32];
+
+  const int g = blockIdx.x, per = a.grid / 8;
+  const int tile = (g % 8) * per + g / 8;
+  if (tile >= a.tiles_m) return;
+  const int row0 = tile * BM;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
+  const int N = a.N;
+
+  {  // prologue: rows, 16-row masks, offset list, neighbour byte offsets
+    const int row = row0 + tid;
+    const int o = row < N ? (a.order ? a.order[row] : row) : 0;
+    ordT[tid] = o;
+    uint32_t src[27];
+    const uint32_t* nrow = a.nbr + (i64)o * 27;
+#pragma unroll
+    for (int v = 0; v < 27; v++) src[v] = row < N ? nrow[v] : EMPTY;
+    uint32_t gm = 0;  // the row's neighbour mask, straight from its table row
+#pragma unroll
+    for (int v = 0; v < 27; v++) {
+      gm |= src[v] == EMPTY ? 0u : 1u << v;
+      srcT[tid * 27 + v] = src[v] == EMPTY ? kOutOfRange : src[v] * (uint32_t)(CI * 2);
+    }
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
+    if ((tid & 15) == 0) gmask[tid >> 4] = gm;
+  }
+  __syncthreads();
+  uint32_t mask = 0;
+#pragma unroll
+  for (int i = 0; i < BM / 16; i++) mask |= gmask[i];
+  const int nvv = __popc(mask);
+  if (tid < 27 && ((mask >> tid) & 1u)) vlist[__popc(mask & ((1u << tid) - 1u))] = tid;
+  uint32_t gms[G];
+#pragma unroll
+  for (int i = 0; i < G; i++) gms[i] = __builtin_amdgcn_readfirstlane(gmask[wv * G + i]);
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes), rw = make_rsrc(a.w, a.w_bytes);
+  f32x4v acc[G][T];
+#pragma unroll
+  for (int i = 0; i < G; i++)
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[i][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int BL = WB / NT;  // weight loads per thread per offset
+  // gathers of offset list entry vi into ra (groups without that offset skip their loads)
+  auto gather = [&](int vi, u32x4 (&ra)[G][S]) __attribute__((always_inline)) {
+    const int v = __builtin_amdgcn_readfirstlane(vlist[vi]);
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      if ((gms[i] >> v) & 1u) {
+        const uint32_t off = srcT[(wv * 64 + i * 16 + r16) * 27 + v] + q4 * (S * 16);
+#pragma unroll
+        for (int m = 0; m < S; m++) ra[i][m] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + m * 16, 0, 0);
+      }
+    }
+  };
+  // MFMAs of offset list entry vi (weights in Bs[buf]); then stage the next offset's weights and synchronise
+  auto compute = [&](int vi, int buf, const u32x4 (&ra)[G][S]) __attribute__((always_inline)) {
+    const int v = __builtin_amdgcn_readfirstlane(vlist[vi]);
+    const int vn = __builtin_amdgcn_readfirstlane(vlist[vi + 1 < nvv ? vi + 1 : vi]);
+    u32x4 rbN[BL];
+#pragma unroll
+    for (int k = 0; k < BL; k++) rbN[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, vn * WB * 16, 0);
+    u32x4 fb[T][S];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int m = 0; m < S; m++) fb[t][m] = Bs[buf][(t * S + m) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      if ((gms[i] >> v) & 1u) {
+#pragma unroll
+        for (int m = 0; m < S; m++)
+#pragma unroll
+          for (int t = 0; t < T; t++) acc[i][t] = mfma16<F16>(ra[i][m], fb[t][m], acc[i][t]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < BL; k++) Bs[buf ^ 1][k * NT + tid] = rbN[k];
+    __syncthreads();
+  };
+  __syncthreads();  // vlist visible
+  if (nvv > 0) {
+    {
+      const int v0 = __builtin_amdgcn_readfirstlane(vlist[0]);
+#pragma unroll
+      for (int k = 0; k < BL; k++) Bs[0][k * NT + tid] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, v0 * WB * 16, 0);
+    }
+    u32x4 ra0[G][S], ra1[G][S];
+    gather(0, ra0);
+    __syncthreads();
+    // software pipeline: the gathers of entry vi+1 are in flight while entry vi computes
+    for (int vi = 0; vi < nvv; vi += 2) {
+      if (vi + 1 < nvv) gather(vi + 1, ra1);
+      compute(vi, 0, ra0);
+      if (vi + 1 >= nvv) break;
+      if (vi + 2 < nvv) gather(vi + 2, ra0);
+      compute(vi + 1, 1, ra1);
+    }
+  }
+
+  // epilogue: per 16-row group through a per-wavefront [16][CO+4] fp32 area (aliases srcT, idle now)
+  constexpr int ES = CO + 4;
+  static_assert(4 * 16 * ES * 4 <= BM * 27 * 4, "epilogue staging fits");
+  float* ew = (float*)srcT + wv * 16 * ES;
+  constexpr int LPR = CO / 8;       // lanes per output row (8 channels each)
+  constexpr int RPP = 64 / LPR;     // rows per pass
+  const int c8 = (lane % LPR) * 8;
+  float bias8[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[c8 + q] : 0.f;
+  // all of this wavefront's residual segments are requested up front (one memory latency, not one per group)
+  constexpr int NP = 16 / RPP;
+  u32x4 resv[G][NP][2];
+  if (a.res) {
+#pragma unroll
+    for (int i = 0; i < G; i++)
+#pragma unroll
+      for (int p = 0; p < NP; p++) {
+        const int lrow = wv * 64 + i * 16 + p * RPP + lane / LPR;
+        const i64 o = (i64)ordT[lrow] * CO + c8;
+        const bool ok = row0 + lrow < N;
+        if (a.res_dt == F32) {
+          resv[i][p][0] = ok ? *(const u32x4*)((const float*)a.res + o) : u32x4{0, 0, 0, 0};
+          resv[i][p][1] = ok ? *(const u32x4*)((const float*)a.res + o + 4) : u32x4{0, 0, 0, 0};
+        } else {
+          resv[i][p][0] = ok ? *(const u32x4*)((const uint16_t*)a.res + o) : u32x4{0, 0, 0, 0};
+        }
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) ew[(q4 * 4 + e) * ES + t * 16 + r16] = acc[i][t][e];
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const int rr = p * RPP + lane / LPR;
+      const int lrow = wv * 64 + i * 16 + rr;
+      if (row0 + lrow >= N) continue;
+      const i64 o = (i64)ordT[lrow] * CO + c8;
+      float v8[8];
+      *(f32x4*)&v8[0] = *(const f32x4*)&ew[rr * ES + c8];
+      *(f32x4*)&v8[4] = *(const f32x4*)&ew[rr * ES + c8 + 4];
+      store_row8_pre(a, o, v8, bias8, resv[i][p]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  }
+}
+
+template <bool F16, int S, int T>
+void launch_narrow(ConvArgs a) {
+  a.tiles_m = cdiv(a.N, 256);
+  a.tiles_n = 1;
+  a.grid = (a.tiles_m + 7) / 8 * 8;
+  k_conv_narrow<F16, S, T><<<a.grid, 256, 0, stream()>>>(a);
+}
+
 template <bool F16, int NW, int BM>
 void launch_wide(ConvArgs a) {
   a.tiles_m = cdiv(a.N, BM);
@@ -549,6 +803,14 @@ void launch(ConvArgs a) {
 
 template <bool F16>
 void dispatch(const SpConvCfg& cfg, ConvArgs a) {
+  if (a.Co == 64 && a.Ci <= 128) {
+    switch (a.Ci / 32) {
+      case 1: return launch_narrow<F16, 1, 4>(a);
+      case 2: return launch_narrow<F16, 2, 4>(a);
+      case 3: return launch_narrow<F16, 3, 4>(a);
+      default: return launch_narrow<F16, 4, 4>(a);
+    }
+  }
   // Fixed tiles per channel width (no autotune): BM = 128 sorted rows per tile.
   if (cfg.BK == 64 && a.Co % 256 == 0) return launch_wide<F16, 4, 256>(a);
   if (cfg.BK == 64 && a.Co % 128 == 0) return launch_wide<F16, 2, 128>(a);
@@ -619,9 +881,14 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   a.Co = Co;
   a.act = act;
   Tensor wpack;
-  if (cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the MFMA-ordered weight copy
+  const i64 chunks = (i64)Co * 27 * Ci / 8;
+  if (Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, rows in spatial order
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
-    i64 chunks = (i64)Co * 27 * Ci / 8;
+    k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
+    a.w = wpack.ptr<uint16_t>();
+    a.order = c.window_order(12).ptr<int32_t>();
+  } else if (cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
+    wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
   }

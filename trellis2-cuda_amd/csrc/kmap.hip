@@ -197,6 +197,28 @@ const Tensor& SpConvCache::block_masks(int B1) {
   return masks.emplace(B1, code).first->second;
 }
 
+__global__ void k_window_keys(const int32_t* __restrict__ sorted, i64 n, int shift, uint32_t* __restrict__ key) {
+  i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) key[i] = (uint32_t)sorted[i] >> shift;
+}
+
+const Tensor& SpConvCache::window_order(int log2w) {
+  auto it = worder.find(log2w);
+  if (it != worder.end()) return it->second;
+  REQ(log2w >= 0 && log2w < 31, "window 2^%d", log2w);
+  Tensor o = empty({std::max<i64>(N, 1)}, I32);
+  if (N) {
+    // sorted is already stable by decoded mask; a stable pass by window index (row >> log2w) keeps that order
+    // inside each window
+    Tensor key = empty({N}, I32);
+    k_window_keys<<<cdiv(N, 256), 256, 0, stream()>>>(sorted.ptr<int32_t>(), N, log2w, key.ptr<uint32_t>());
+    int bits = 1;
+    while (bits < 31 && ((i64)(N - 1) >> log2w) >> bits) bits++;
+    stable_sort_pairs(key.ptr<uint32_t>(), sorted.ptr<int32_t>(), N, bits, o.ptr<int32_t>());
+  }
+  return worder.emplace(log2w, o).first->second;
+}
+
 const std::pair<Tensor, Tensor>& SpConvCache::valid(int B1) {
   auto it = vk.find(B1);
   if (it != vk.end()) return it->second;

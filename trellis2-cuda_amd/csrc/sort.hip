@@ -83,25 +83,31 @@ __global__ void __launch_bounds__(RT) k_rs_scatter(const uint32_t* __restrict__ 
 }
 }  // namespace
 
-void stable_argsort27(const uint32_t* keys, i64 n, int32_t* order) {
+void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bits, int32_t* vals_out) {
   if (n <= 0) return;
   REQ(n < (1ll << 31), "sort size %lld", (long long)n);
+  REQ(bits >= 1 && bits <= 32, "key bits %d", bits);
+  const int passes = (bits + RBITS - 1) / RBITS;
   int ntiles = cdiv(n, RTILE);
   i64 nh = (i64)NBUK * ntiles;
-  Tensor hist = empty({nh}, I32), kb0 = empty({n}, I32), kb1 = empty({n}, I32), vb = empty({n}, I32);
+  Tensor hist = empty({nh}, I32), kb0 = empty({n}, I32), kb1 = empty({n}, I32), vb0 = empty({n}, I32),
+         vb1 = empty({n}, I32);
   hipStream_t s = stream();
-  // pass p reads (kin, vin) and writes (kout, vout); the last pass writes the values straight into `order`
+  // ping-pong buffers; the last pass writes its values straight into vals_out
   const uint32_t* kin = keys;
-  const int32_t* vin = nullptr;
-  uint32_t* kouts[3] = {kb0.ptr<uint32_t>(), kb1.ptr<uint32_t>(), kb0.ptr<uint32_t>()};
-  int32_t* vouts[3] = {order, vb.ptr<int32_t>(), order};
-  for (int p = 0; p < 3; p++) {
+  const int32_t* vin = vals;
+  for (int p = 0; p < passes; p++) {
+    const bool last = p + 1 == passes;
+    uint32_t* kout = (p & 1) ? kb1.ptr<uint32_t>() : kb0.ptr<uint32_t>();
+    int32_t* vout = last ? vals_out : ((p & 1) ? vb1.ptr<int32_t>() : vb0.ptr<int32_t>());
     int shift = p * RBITS;
     k_rs_count<<<ntiles, RT, 0, s>>>(kin, n, shift, hist.ptr<uint32_t>(), ntiles);
     excl_scan_u32(hist.ptr<uint32_t>(), hist.ptr<uint32_t>(), nh, nullptr);
-    k_rs_scatter<<<ntiles, RT, 0, s>>>(kin, vin, kouts[p], vouts[p], n, shift, hist.ptr<uint32_t>(), ntiles);
-    kin = kouts[p];
-    vin = vouts[p];
+    k_rs_scatter<<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, hist.ptr<uint32_t>(), ntiles);
+    kin = kout;
+    vin = vout;
   }
   CK(hipGetLastError());
 }
+
+void stable_argsort27(const uint32_t* keys, i64 n, int32_t* order) { stable_sort_pairs(keys, nullptr, n, 27, order); }

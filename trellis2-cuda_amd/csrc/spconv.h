@@ -21,6 +21,11 @@ struct SpConvCache {
   // bits of masks[b] are exactly list[seg[b]:seg[b+1]].
   std::map<int, Tensor> masks;
   const Tensor& block_masks(int B1);
+  // Rows grouped by spatial window (row >> log2w, i.e. runs of 2^log2w rows of the input order) and, inside a
+  // window, in the gray-sorted order: neighbour masks stay similar within small row groups while the rows a tile
+  // gathers stay spatially close. Used by the narrow-channel kernels.
+  std::map<int, Tensor> worder;
+  const Tensor& window_order(int log2w);
 };
 SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D);  // coords int32 [N,4] (b,x,y,z)
 
