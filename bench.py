@@ -45,7 +45,17 @@ def main():
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 1 GiB device-to-device copy (the counter calibration used by bench_profile.py)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box has one GPU).",
               file=sys.stderr)
@@ -124,12 +134,16 @@ def main():
     gbs = comp_bytes / (ms * 1e-3) / 1e9
     mvox = n / (ms * 1e-3) / 1e6
     wide = ci >= 256 or co >= 256
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{cfg.name}.json")
+    if os.path.exists(tfile):  # HBM bytes per launch measured by bench_profile.py (FETCH_SIZE + WRITE_SIZE)
+        traffic = round(json.load(open(tfile))["traffic_bytes"])
     if wide:
         roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None}
+                "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
     else:
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic}
 
     cpu = None
     if not args.no_cpu:
@@ -141,11 +155,16 @@ def main():
         bs = b.cpu().numpy()
         rs = res.float().cpu().numpy() if res is not None else None
         rng = np.random.default_rng(0)
-        rows = rng.choice(n, size=min(n, 256), replace=False)
-        t = time.perf_counter()
-        oracle.conv(xs, ws, bs, onbr, res=rs, act=act, rows=rows, nthreads=nt)
-        pilot = time.perf_counter() - t
-        k = int(min(n, max(256, 256 * args.cpu_seconds / max(pilot, 1e-3))))
+        k = 256
+        while True:  # grow the pilot until it runs long enough to time, then scale to the requested duration
+            rows = rng.choice(n, size=min(n, k), replace=False)
+            t = time.perf_counter()
+            oracle.conv(xs, ws, bs, onbr, res=rs, act=act, rows=rows, nthreads=nt)
+            pilot = time.perf_counter() - t
+            if pilot > 0.5 or k >= n:
+                break
+            k *= 4
+        k = int(min(n, max(256, k * args.cpu_seconds / max(pilot, 1e-3))))
         rows = rng.choice(n, size=k, replace=False)
         t = time.perf_counter()
         oracle.conv(xs, ws, bs, onbr, res=rs, act=act, rows=rows, nthreads=nt)
@@ -157,7 +176,7 @@ def main():
                "mvox_per_s": round(k / cs / 1e6, 4)}
 
     out = {
-        "metric": "sparse-conv effective TFLOPS at 256^3 C=256 bf16 (active-pair flops)",
+        "metric": "sparse-conv effective TFLOPS + Mvoxels/s at 256^3 C=256 bf16; % MFMA/HBM peak",
         "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (seeded union-of-shapes shell, random N(0,1) features)",
