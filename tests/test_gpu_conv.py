@@ -168,3 +168,13 @@ def test_c5_children(gpu):
     c = gc.cpu().numpy()
     rows = np.sort(np.random.default_rng(2).choice(len(c), size=1500, replace=False))
     run_case(gpu, c, cfg.ci, cfg.co, act=1, rows=rows, seed=cfg.seed)
+
+
+def test_conv_golden_fixture(gpu):
+    """Against tests/golden/small_shell.npz: y = silu(conv(x, w) + b) + r from float64 torch conv3d (Ci=32, Co=64)."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "small_shell.npz"))
+    t = lambda k: torch.from_numpy(g[k]).to(gpu).view(torch.bfloat16)
+    cache = sp.build_neighbors(torch.from_numpy(g["coords"]).to(gpu))
+    y = sp.subm_conv_fused(t("x"), t("w"), t("b"), cache, residual=t("r"), act=sp.ACT_SILU, out_dtype=torch.float32)
+    compare(y, g["y_silu_res"].astype(np.float32), "f32", "golden fixture")

@@ -107,3 +107,17 @@ def test_subdivide(gpu, name):
     gc, gs = sp.subdivide(tc, tl)
     np.testing.assert_array_equal(gc.cpu().numpy(), oc)
     np.testing.assert_array_equal(gs.cpu().numpy(), osrc)
+
+
+def test_kmap_golden_fixture(gpu):
+    """Against tests/golden/small_shell.npz (brute-force kernel map, shuffled rows, two batches)."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "small_shell.npz"))
+    cache, nbr, gray, srt = gpu_map(g["coords"], gpu)
+    np.testing.assert_array_equal(nbr, g["nbr"])
+    np.testing.assert_array_equal(gray, g["gray"])
+    np.testing.assert_array_equal(srt, g["order"])
+    for B1 in (32, 128):
+        lst, seg = cache.valid(B1)
+        np.testing.assert_array_equal(lst.cpu().numpy(), g[f"list{B1}"])
+        np.testing.assert_array_equal(seg.cpu().numpy(), g[f"seg{B1}"])

@@ -184,3 +184,31 @@ def test_subdivide():
     np.testing.assert_array_equal(oc, np.array(exp_c, np.int32).reshape(-1, 4))
     np.testing.assert_array_equal(src, exp_s)
     np.testing.assert_array_equal(oc[:, 1:] // 2, c[src // 8, 1:])
+
+
+# ------------------------------------------------------------------------------------------ golden fixture
+def load_golden():
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "small_shell.npz"))
+    return {k: d[k] for k in d.files}
+
+
+def bf16_bits_to_f32(a):
+    return (a.astype(np.int32).astype(np.uint32) << 16).view(np.float32)
+
+
+def test_oracle_matches_golden_fixture():
+    """tests/golden/small_shell.npz was written by brute force and torch conv3d, not by the oracle."""
+    g = load_golden()
+    nbr, gray, binv, srt = oracle.build_neighbors(g["coords"])
+    np.testing.assert_array_equal(nbr, g["nbr"])
+    np.testing.assert_array_equal(gray, g["gray"])
+    np.testing.assert_array_equal(binv, g["dec"])
+    np.testing.assert_array_equal(srt, g["order"])
+    for B1 in (32, 128):
+        lst, seg = oracle.valid(gray, srt, B1)
+        np.testing.assert_array_equal(lst, g[f"list{B1}"])
+        np.testing.assert_array_equal(seg, g[f"seg{B1}"])
+    x, w, b, r = (bf16_bits_to_f32(g[k]) for k in ("x", "w", "b", "r"))
+    y = oracle.conv(x, w, b, nbr, res=r, act=1)
+    np.testing.assert_allclose(y, g["y_silu_res"], rtol=1e-5, atol=1e-5)
