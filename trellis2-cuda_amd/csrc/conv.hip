@@ -755,6 +755,221 @@ void launch_narrow(ConvArgs a) {
   k_conv_narrow<F16, S, T><<<a.grid, 256, 0, stream()>>>(a);
 }
 
+// vmcnt-only s_waitcnt (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14])
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Workgroup barrier without the memory fence of __syncthreads(): that fence waits for every outstanding vector
+// load (vmcnt(0)), including LDS-DMA prefetches meant to stay in flight. Callers order LDS data themselves
+// (counted vmcnt waits); the empty asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Wide-channel kernel, 256 sorted rows x 256 channels per workgroup (4 wavefronts, each all 256 rows x 64
+// channels = 8 x 2 tiles of 32x32 fp32 accumulators in AGPRs). Differences from k_conv_wide:
+//  * The gathered A tile goes global -> LDS directly (buffer_load ... lds, 16 bytes per lane; EMPTY neighbours
+//    read past the buffer end and land as zeros) into a 4-slot LDS ring, 3 stages ahead of the MFMAs: no
+//    registers hold gathers in flight, and gather latency hides behind three stages of MFMA work. The slots are
+//    four distinct LDS objects so the compiler can tell the DMA into one slot from the reads of another.
+//  * Ring protocol per stage s: wait (counted vmcnt) for this lane's DMA of A(s), barrier (every wavefront's
+//    part has landed and everyone is done with stage s-1), then, between the MFMA groups of stage s, refill the
+//    slot stage s-1 used with A(s+3) and load the weights of stage s+1 into the other register set.
+template <bool F16>
+__global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
+  constexpr int NW = 4, NT = 256, BM = 256, KC = 64, PC = KC / 8;
+  constexpr int TM = 8, TN = 2, AL = BM * PC / NT;  // AL = 8 DMA loads per lane per stage
+  __shared__ __attribute__((aligned(16))) u32x4 As0[BM * PC], As1[BM * PC], As2[BM * PC], As3[BM * PC];
+  __shared__ uint32_t srcT[BM * 27];
+  __shared__ int ordT[BM];
+  __shared__ uint32_t gmask[TM];
+  __shared__ int vlist[32];
+
+  const int g = blockIdx.x, per = a.grid / 8;
+  const int logical = (g % 8) * per + g / 8;
+  if (logical >= a.tiles_m * a.tiles_n) return;
+  const int tm_ = logical / a.tiles_n, tn_ = logical % a.tiles_n;
+  const int row0 = tm_ * BM, co0 = tn_ * (64 * NW);
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = a.N, Ci = a.Ci, nkc = Ci / KC;
+
+  {  // prologue: row indices, 32-row masks, neighbour byte offsets (one row per thread)
+    const int row = row0 + tid;
+    const int o = row < N ? a.order[row] : 0;
+    ordT[tid] = o;
+    uint32_t src[27];
+    const uint32_t* nrow = a.nbr + (i64)o * 27;
+#pragma unroll
+    for (int v = 0; v < 27; v++) src[v] = row < N ? nrow[v] : EMPTY;
+    uint32_t gm = 0;
+#pragma unroll
+    for (int v = 0; v < 27; v++) {
+      gm |= src[v] == EMPTY ? 0u : 1u << v;
+      srcT[tid * 27 + v] = src[v] == EMPTY ? kOutOfRange : src[v] * (uint32_t)(Ci * 2);
+    }
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
+    if ((tid & 31) == 0) gmask[tid >> 5] = gm;
+  }
+  __syncthreads();
+  uint32_t mask = 0;
+#pragma unroll
+  for (int i = 0; i < TM; i++) mask |= gmask[i];
+  const int nvv = __popc(mask), total = nvv * nkc;
+  if (tid < 27 && ((mask >> tid) & 1u)) vlist[__popc(mask & ((1u << tid) - 1u))] = tid;
+  uint32_t gms[TM];
+#pragma unroll
+  for (int i = 0; i < TM; i++) gms[i] = __builtin_amdgcn_readfirstlane(gmask[i]);
+  __syncthreads();
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes), rw = make_rsrc(a.w, a.w_bytes);
+  // DMA k of this lane fills LDS unit u = (wn*AL + k)*64 + lane: row u/8, slot u%8, channel piece
+  // slot ^ ((row >> 1) & 7)
+  uint32_t drow[AL], dpiece[AL];
+#pragma unroll
+  for (int k = 0; k < AL; k++) {
+    const int u = (wn * AL + k) * 64 + lane;
+    drow[k] = u >> 3;
+    dpiece[k] = (u & 7) ^ ((u >> 4) & 7);
+  }
+  const uint32_t wslice = (uint32_t)((co0 >> 6) + wn) * 27u * (uint32_t)nkc;
+  const uint32_t wlane = (uint32_t)lane * 16u;
+
+  int avi = 0, akc = 0, bvi = 0, bkc = 0, cvi = 0, ckc = 0;
+  auto next = [&](int& vi, int& kc) __attribute__((always_inline)) {
+    const bool wrap = kc + 1 == nkc;
+    kc = wrap ? 0 : kc + 1;
+    vi += wrap ? 1 : 0;
+  };
+  // DMA addresses of the next A stage (offset entry avi, channel block akc; clamped to the last stage)
+  auto a_offsets = [&](uint32_t (&off)[AL], int& ka) __attribute__((always_inline)) {
+    const bool live = avi < nvv;
+    const int va = __builtin_amdgcn_readfirstlane(vlist[live ? avi : nvv - 1]);
+    ka = __builtin_amdgcn_readfirstlane((live ? akc : nkc - 1) * KC * 2);
+    next(avi, akc);
+#pragma unroll
+    for (int k = 0; k < AL; k++) off[k] = srcT[drow[k] * 27 + va] + dpiece[k] * 16;
+  };
+  auto dma = [&](u32x4* slot, int k, uint32_t off, int ka) __attribute__((always_inline)) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)&slot[(wn * AL + k) * 64],
+                                             16, off, ka, 0, 0);
+  };
+  auto b_base = [&]() __attribute__((always_inline)) {
+    const bool live = bvi < nvv;
+    const int vb = __builtin_amdgcn_readfirstlane(vlist[live ? bvi : nvv - 1]);
+    const int kb = live ? bkc : nkc - 1;
+    next(bvi, bkc);
+    return __builtin_amdgcn_readfirstlane((int)((wslice + (uint32_t)(vb * nkc + kb)) * 8192u));
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int t = 0; t < TN; t++) acc[i][t] = f32x16{};
+
+  // one K stage: MFMAs from slot `cur` and weights rbC; DMA A(s+3) into `fill`; weights of s+1 into rbN
+  auto stage = [&](const u32x4* cur, u32x4* fill, const u32x4 (&rbC)[TN][4], u32x4 (&rbN)[TN][4])
+      __attribute__((always_inline)) {
+    const uint32_t vbit = 1u << __builtin_amdgcn_readfirstlane(vlist[cvi]);
+    next(cvi, ckc);
+    uint32_t off[AL];
+    int ka;
+    a_offsets(off, ka);
+    const int soff = b_base();
+    u32x4 fa[2][4];
+    auto read_fa = [&](u32x4 (&f)[4], int i) __attribute__((always_inline)) {
+      const int r = i * 32 + l32;
+#pragma unroll
+      for (int j = 0; j < 4; j++) f[j] = cur[r * PC + ((h * 4 + j) ^ ((r >> 1) & 7))];
+    };
+    read_fa(fa[0], 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      dma(fill, i, off[i], ka);
+      rbN[i / 4][i % 4] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + i * 1024, soff, 0);
+      if (i + 1 < TM) read_fa(fa[(i + 1) & 1], i + 1);
+      if (gms[i] & vbit) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int t = 0; t < TN; t++) acc[i][t] = mfma32<F16>(fa[i & 1][j], rbC[t][j], acc[i][t]);
+      }
+    }
+  };
+  // loads issued after this lane's last DMA of A(s) when stage s starts: prologue DMAs and B(0) for s < 3,
+  // then (in steady state) one weight load of stage s-3 plus two full stages of 16
+  auto wait_a = [&](int s) __attribute__((always_inline)) {
+    if (s == 0) wait_vmcnt<2 * AL + 8>();
+    else if (s == 1) wait_vmcnt<AL + 8 + 16>();
+    else if (s == 2) wait_vmcnt<8 + 2 * 16>();
+    else wait_vmcnt<1 + 2 * 16>();
+  };
+
+  if (total > 0) {
+    u32x4 rb0[TN][4], rb1[TN][4];
+    {
+      uint32_t off[AL];
+      int ka;
+      a_offsets(off, ka);
+#pragma unroll
+      for (int k = 0; k < AL; k++) dma(As0, k, off[k], ka);
+      a_offsets(off, ka);
+#pragma unroll
+      for (int k = 0; k < AL; k++) dma(As1, k, off[k], ka);
+      a_offsets(off, ka);
+#pragma unroll
+      for (int k = 0; k < AL; k++) dma(As2, k, off[k], ka);
+      const int soff = b_base();
+#pragma unroll
+      for (int q = 0; q < 8; q++) rb0[q / 4][q % 4] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + q * 1024, soff, 0);
+    }
+    for (int s = 0; s < total; s += 4) {
+      wait_a(s);
+      wg_barrier();
+      stage(As0, As3, rb0, rb1);
+      if (s + 1 >= total) break;
+      wait_a(s + 1);
+      wg_barrier();
+      stage(As1, As0, rb1, rb0);
+      if (s + 2 >= total) break;
+      wait_a(s + 2);
+      wg_barrier();
+      stage(As2, As1, rb0, rb1);
+      if (s + 3 >= total) break;
+      wait_a(s + 3);
+      wg_barrier();
+      stage(As3, As2, rb1, rb0);
+    }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  // epilogue through this wavefront's share of the (now idle) ring
+  float* ew = (wn < 2 ? (float*)&As0[0] : (float*)&As1[0]) + (wn & 1) * (32 * 72);
+  static_assert(2 * 32 * 72 * 4 <= BM * PC * 16, "two wavefronts' epilogue staging fits in one ring slot");
+  const int co_w = co0 + wn * 64;
+  float bias8[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[co_w + (lane & 7) * 8 + q] : 0.f;
+  const int nrows = N - row0;
+  static_for<TM>([&](auto I) { epilogue_group<TN>(acc[I], ew, ordT, I * 32, nrows, co_w, bias8, a, lane); });
+}
+
+template <bool F16>
+void launch_wide_dma(ConvArgs a) {
+  a.tiles_m = cdiv(a.N, 256);
+  a.tiles_n = a.Co / 256;
+  int tiles = a.tiles_m * a.tiles_n;
+  a.grid = (tiles + 7) / 8 * 8;
+  k_conv_wide_dma<F16><<<a.grid, 256, 0, stream()>>>(a);
+}
+
 template <bool F16, int NW, int BM>
 void launch_wide(ConvArgs a) {
   a.tiles_m = cdiv(a.N, BM);
@@ -812,7 +1027,7 @@ void dispatch(const SpConvCfg& cfg, ConvArgs a) {
     }
   }
   // Fixed tiles per channel width (no autotune): BM = 128 sorted rows per tile.
-  if (cfg.BK == 64 && a.Co % 256 == 0) return launch_wide<F16, 4, 256>(a);
+  if (cfg.BK == 64 && a.Co % 256 == 0) return launch_wide_dma<F16>(a);
   if (cfg.BK == 64 && a.Co % 128 == 0) return launch_wide<F16, 2, 128>(a);
   if (a.Co % 128 == 0) {
     if (cfg.BK == 64) launch<F16, 128, 128, 2, 2, 64>(a);
