@@ -19,6 +19,8 @@
 
 #include "spconv.h"
 
+
+
 namespace {
 constexpr uint32_t EMPTY = 0xffffffffu;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -584,9 +586,9 @@ __global__ void k_pack_w_narrow(const u32x4* __restrict__ w, u32x4* __restrict__
 //    MFMAs for it. Rows come in the order the caller chooses (null = identity); the spatial (Morton) order keeps
 //    the gathers of neighbouring rows in L2.
 //  * Epilogue: per 16-row group, accumulators go through LDS and leave as 16-byte segments of whole output rows.
-template <bool F16, int S, int T>
+template <bool F16, int S, int T, int G>
 __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
-  constexpr int BM = 256, NT = 256, G = 4, CI = 32 * S, CO = 16 * T, WB = T * S * 64;  // WB: 16B units per offset
+  constexpr int NT = 256, BM = 4 * 16 * G, CI = 32 * S, CO = 16 * T, WB = T * S * 64;  // WB: 16B units per offset
   static_assert(WB % NT == 0, "weight slice split");
   __shared__ __attribute__((aligned(16))) u32x4 Bs[2][WB];
   __shared__ __attribute__((aligned(16))) uint32_t srcT[BM * 27];
@@ -601,7 +603,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
   const int N = a.N;
 
-  {  // prologue: rows, 16-row masks, offset list, neighbour byte offsets
+  if (tid < BM) {  // prologue: rows, 16-row masks, offset list, neighbour byte offsets
     const int row = row0 + tid;
     const int o = row < N ? (a.order ? a.order[row] : row) : 0;
     ordT[tid] = o;
@@ -643,7 +645,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 #pragma unroll
     for (int i = 0; i < G; i++) {
       if ((gms[i] >> v) & 1u) {
-        const uint32_t off = srcT[(wv * 64 + i * 16 + r16) * 27 + v] + q4 * (S * 16);
+        const uint32_t off = srcT[(wv * (16 * G) + i * 16 + r16) * 27 + v] + q4 * (S * 16);
 #pragma unroll
         for (int m = 0; m < S; m++) ra[i][m] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + m * 16, 0, 0);
       }
@@ -696,8 +698,11 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 
   // epilogue: per 16-row group through a per-wavefront [16][CO+4] fp32 area (aliases srcT, idle now)
   constexpr int ES = CO + 4;
-  static_assert(4 * 16 * ES * 4 <= BM * 27 * 4, "epilogue staging fits");
-  float* ew = (float*)srcT + wv * 16 * ES;
+  // staging: the neighbour table or the weight buffers, whichever holds 4 x [16][ES] floats (both idle now)
+  constexpr bool kInSrcT = 4 * 16 * ES * 4 <= BM * 27 * 4;
+  static_assert(kInSrcT || 4 * 16 * ES * 4 <= 2 * WB * 16, "epilogue staging fits");
+  __syncthreads();  // every wavefront is done with the table and the weight buffers
+  float* ew = (kInSrcT ? (float*)srcT : (float*)&Bs[0][0]) + wv * 16 * ES;
   constexpr int LPR = CO / 8;       // lanes per output row (8 channels each)
   constexpr int RPP = 64 / LPR;     // rows per pass
   const int c8 = (lane % LPR) * 8;
@@ -712,7 +717,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
     for (int i = 0; i < G; i++)
 #pragma unroll
       for (int p = 0; p < NP; p++) {
-        const int lrow = wv * 64 + i * 16 + p * RPP + lane / LPR;
+        const int lrow = wv * (16 * G) + i * 16 + p * RPP + lane / LPR;
         const i64 o = (i64)ordT[lrow] * CO + c8;
         const bool ok = row0 + lrow < N;
         if (a.res_dt == F32) {
@@ -734,7 +739,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 #pragma unroll
     for (int p = 0; p < NP; p++) {
       const int rr = p * RPP + lane / LPR;
-      const int lrow = wv * 64 + i * 16 + rr;
+      const int lrow = wv * (16 * G) + i * 16 + rr;
       if (row0 + lrow >= N) continue;
       const i64 o = (i64)ordT[lrow] * CO + c8;
       float v8[8];
@@ -749,10 +754,11 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 
 template <bool F16, int S, int T>
 void launch_narrow(ConvArgs a) {
-  a.tiles_m = cdiv(a.N, 256);
+  constexpr int G = S <= 2 ? 4 : 2;  // 16-row groups per wavefront: keeps two wavefronts per SIMD at Ci = 128
+  a.tiles_m = cdiv(a.N, 4 * 16 * G);
   a.tiles_n = 1;
   a.grid = (a.tiles_m + 7) / 8 * 8;
-  k_conv_narrow<F16, S, T><<<a.grid, 256, 0, stream()>>>(a);
+  k_conv_narrow<F16, S, T, G><<<a.grid, 256, 0, stream()>>>(a);
 }
 
 // vmcnt-only s_waitcnt (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14])
