@@ -28,6 +28,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte load/store unit (native vector, not a struct)
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {  // round to nearest even, quiet NaN preserved
@@ -71,6 +72,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
 }
 
+// vmcnt-only s_waitcnt (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14])
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Workgroup barrier without the memory fence of __syncthreads(): that fence waits for every outstanding vector
+// load (vmcnt(0)), including LDS-DMA prefetches meant to stay in flight. Callers order LDS data themselves
+// (counted vmcnt waits); the empty asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 struct ConvArgs {
   const uint16_t* x;
   const uint16_t* w;
@@ -83,7 +99,7 @@ struct ConvArgs {
   const uint32_t* code;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
-  uint32_t x_bytes, w_bytes;
+  uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes;
 };
 
 template <bool F16, int BM, int BN, int WGM, int WGN, int KC>
@@ -591,8 +607,10 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   constexpr int NT = 256, BM = 4 * 16 * G, CI = 32 * S, CO = 16 * T, WB = T * S * 64;  // WB: 16B units per offset
   static_assert(WB % NT == 0, "weight slice split");
   __shared__ __attribute__((aligned(16))) u32x4 Bs[2][WB];
-  __shared__ __attribute__((aligned(16))) uint32_t srcT[BM * 27];
+  constexpr int SR = 28;  // srcT row stride: 27 offsets padded to 7 x 16 bytes
+  __shared__ __attribute__((aligned(16))) uint32_t srcT[BM * SR];
   __shared__ int ordT[BM];
+  __shared__ __attribute__((aligned(16))) u32x4 resL[BM * CO * 2 / 16];
   __shared__ uint32_t gmask[BM / 16];
   __shared__ int vlist[32];
 
@@ -605,18 +623,35 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 
   if (tid < BM) {  // prologue: rows, 16-row masks, offset list, neighbour byte offsets
     const int row = row0 + tid;
-    const int o = row < N ? (a.order ? a.order[row] : row) : 0;
+    const bool live = row < N;
+    const int o = live ? (a.order ? a.order[row] : row) : 0;
     ordT[tid] = o;
-    uint32_t src[27];
-    const uint32_t* nrow = a.nbr + (i64)o * 27;
+    // the row's 27 neighbour indices: one contiguous 108-byte run, fetched as 6 x 16 + 12 bytes
+    const __amdgpu_buffer_rsrc_t rn = make_rsrc(a.nbr, a.nbr_bytes);
+    uint32_t src[28];
 #pragma unroll
-    for (int v = 0; v < 27; v++) src[v] = row < N ? nrow[v] : EMPTY;
+    for (int j = 0; j < 6; j++) {
+      const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rn, (uint32_t)o * 108u + j * 16, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; e++) src[j * 4 + e] = q[e];
+    }
+    {
+      const u32x3 q = __builtin_amdgcn_raw_buffer_load_b96(rn, (uint32_t)o * 108u + 96, 0, 0);
+      src[24] = q[0];
+      src[25] = q[1];
+      src[26] = q[2];
+      src[27] = EMPTY;
+    }
     uint32_t gm = 0;  // the row's neighbour mask, straight from its table row
 #pragma unroll
-    for (int v = 0; v < 27; v++) {
-      gm |= src[v] == EMPTY ? 0u : 1u << v;
-      srcT[tid * 27 + v] = src[v] == EMPTY ? kOutOfRange : src[v] * (uint32_t)(CI * 2);
+    for (int v = 0; v < 28; v++) {
+      const bool e = !live || src[v] == EMPTY;
+      if (v < 27) gm |= e ? 0u : 1u << v;
+      src[v] = e ? kOutOfRange : src[v] * (uint32_t)(CI * 2);
     }
+#pragma unroll
+    for (int j = 0; j < 7; j++)
+      *(u32x4*)&srcT[tid * SR + j * 4] = u32x4{src[j * 4], src[j * 4 + 1], src[j * 4 + 2], src[j * 4 + 3]};
 #pragma unroll
     for (int d = 1; d < 16; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
     if ((tid & 15) == 0) gmask[tid >> 4] = gm;
@@ -642,22 +677,25 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   // gathers of offset list entry vi into ra (groups without that offset skip their loads)
   auto gather = [&](int vi, u32x4 (&ra)[G][S]) __attribute__((always_inline)) {
     const int v = __builtin_amdgcn_readfirstlane(vlist[vi]);
+    uint32_t off[G];  // all groups' row offsets first: one LDS round trip, not one per group
+#pragma unroll
+    for (int i = 0; i < G; i++) off[i] = srcT[(wv * (16 * G) + i * 16 + r16) * SR + v] + q4 * (S * 16);
 #pragma unroll
     for (int i = 0; i < G; i++) {
       if ((gms[i] >> v) & 1u) {
-        const uint32_t off = srcT[(wv * (16 * G) + i * 16 + r16) * 27 + v] + q4 * (S * 16);
 #pragma unroll
-        for (int m = 0; m < S; m++) ra[i][m] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + m * 16, 0, 0);
+        for (int m = 0; m < S; m++) ra[i][m] = __builtin_amdgcn_raw_buffer_load_b128(rx, off[i] + m * 16, 0, 0);
       }
     }
   };
-  // MFMAs of offset list entry vi (weights in Bs[buf]); then stage the next offset's weights and synchronise
-  auto compute = [&](int vi, int buf, const u32x4 (&ra)[G][S]) __attribute__((always_inline)) {
+  // MFMAs of offset list entry vi (weights in Bs[buf]); the weights of entry vi+2 are requested into rbL, the
+  // ones of entry vi+1 (requested an iteration earlier, in rbS) are stored into the other buffer, then barrier
+  auto compute = [&](int vi, int buf, const u32x4 (&ra)[G][S], u32x4 (&rbL)[BL], const u32x4 (&rbS)[BL])
+      __attribute__((always_inline)) {
     const int v = __builtin_amdgcn_readfirstlane(vlist[vi]);
-    const int vn = __builtin_amdgcn_readfirstlane(vlist[vi + 1 < nvv ? vi + 1 : vi]);
-    u32x4 rbN[BL];
+    const int vn = __builtin_amdgcn_readfirstlane(vlist[vi + 2 < nvv ? vi + 2 : nvv - 1]);
 #pragma unroll
-    for (int k = 0; k < BL; k++) rbN[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, vn * WB * 16, 0);
+    for (int k = 0; k < BL; k++) rbL[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, vn * WB * 16, 0);
     u32x4 fb[T][S];
 #pragma unroll
     for (int t = 0; t < T; t++)
@@ -673,26 +711,48 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
       }
     }
 #pragma unroll
-    for (int k = 0; k < BL; k++) Bs[buf ^ 1][k * NT + tid] = rbN[k];
+    for (int k = 0; k < BL; k++) Bs[buf ^ 1][k * NT + tid] = rbS[k];
     __syncthreads();
   };
+  constexpr int LPR = CO / 8;    // epilogue: lanes per output row (8 channels each)
+  constexpr int RPP = 64 / LPR;   // epilogue: rows per pass
+  const int c8 = (lane % LPR) * 8;
+  // 16-bit residuals: the workgroup's [BM][CO] residual tile goes global -> LDS by DMA before the K loop (its
+  // latency hides behind the loop; no registers held). Rows past N read out of range and land as zeros.
+  constexpr int RU = BM * CO * 2 / 16, RK = RU / NT;  // 16-byte units, DMA loads per lane
+  static_assert(RK * NT == RU, "residual tile split");
+  const bool res16 = a.res && a.res_dt != F32;
+  if (res16) {
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, a.res_bytes);
+#pragma unroll
+    for (int k = 0; k < RK; k++) {
+      const int u = (wv * RK + k) * 64 + lane, rrow = u / LPR, seg = u % LPR;
+      const uint32_t off = row0 + rrow < N ? ((uint32_t)ordT[rrow] * CO + seg * 8) * 2u : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)&resL[(wv * RK + k) * 64],
+                                               16, off, 0, 0, 0);
+    }
+  }
   __syncthreads();  // vlist visible
   if (nvv > 0) {
+    u32x4 rb0[BL], rb1[BL];
     {
       const int v0 = __builtin_amdgcn_readfirstlane(vlist[0]);
+      const int v1 = __builtin_amdgcn_readfirstlane(vlist[nvv > 1 ? 1 : 0]);
 #pragma unroll
       for (int k = 0; k < BL; k++) Bs[0][k * NT + tid] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, v0 * WB * 16, 0);
+#pragma unroll
+      for (int k = 0; k < BL; k++) rb1[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, v1 * WB * 16, 0);
     }
     u32x4 ra0[G][S], ra1[G][S];
     gather(0, ra0);
     __syncthreads();
-    // software pipeline: the gathers of entry vi+1 are in flight while entry vi computes
+    // software pipeline: gathers of entry vi+1 and weights of entry vi+2 are in flight while entry vi computes
     for (int vi = 0; vi < nvv; vi += 2) {
       if (vi + 1 < nvv) gather(vi + 1, ra1);
-      compute(vi, 0, ra0);
+      compute(vi, 0, ra0, rb0, rb1);
       if (vi + 1 >= nvv) break;
       if (vi + 2 < nvv) gather(vi + 2, ra0);
-      compute(vi + 1, 1, ra1);
+      compute(vi + 1, 1, ra1, rb1, rb0);
     }
   }
 
@@ -703,16 +763,12 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   static_assert(kInSrcT || 4 * 16 * ES * 4 <= 2 * WB * 16, "epilogue staging fits");
   __syncthreads();  // every wavefront is done with the table and the weight buffers
   float* ew = (kInSrcT ? (float*)srcT : (float*)&Bs[0][0]) + wv * 16 * ES;
-  constexpr int LPR = CO / 8;       // lanes per output row (8 channels each)
-  constexpr int RPP = 64 / LPR;     // rows per pass
-  const int c8 = (lane % LPR) * 8;
   float bias8[8];
 #pragma unroll
   for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[c8 + q] : 0.f;
-  // all of this wavefront's residual segments are requested up front (one memory latency, not one per group)
   constexpr int NP = 16 / RPP;
   u32x4 resv[G][NP][2];
-  if (a.res) {
+  if (a.res && !res16) {  // fp32 residual: straight to registers, all requested before the first group
 #pragma unroll
     for (int i = 0; i < G; i++)
 #pragma unroll
@@ -720,13 +776,13 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
         const int lrow = wv * (16 * G) + i * 16 + p * RPP + lane / LPR;
         const i64 o = (i64)ordT[lrow] * CO + c8;
         const bool ok = row0 + lrow < N;
-        if (a.res_dt == F32) {
-          resv[i][p][0] = ok ? *(const u32x4*)((const float*)a.res + o) : u32x4{0, 0, 0, 0};
-          resv[i][p][1] = ok ? *(const u32x4*)((const float*)a.res + o + 4) : u32x4{0, 0, 0, 0};
-        } else {
-          resv[i][p][0] = ok ? *(const u32x4*)((const uint16_t*)a.res + o) : u32x4{0, 0, 0, 0};
-        }
+        resv[i][p][0] = ok ? *(const u32x4*)((const float*)a.res + o) : u32x4{0, 0, 0, 0};
+        resv[i][p][1] = ok ? *(const u32x4*)((const float*)a.res + o + 4) : u32x4{0, 0, 0, 0};
       }
+  }
+  if (res16) {
+    wait_vmcnt<0>();
+    __syncthreads();  // every wavefront's residual DMA has landed
   }
 #pragma unroll
   for (int i = 0; i < G; i++) {
@@ -745,6 +801,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
       float v8[8];
       *(f32x4*)&v8[0] = *(const f32x4*)&ew[rr * ES + c8];
       *(f32x4*)&v8[4] = *(const f32x4*)&ew[rr * ES + c8 + 4];
+      if (res16) resv[i][p][0] = resL[lrow * LPR + lane % LPR];
       store_row8_pre(a, o, v8, bias8, resv[i][p]);
     }
     __builtin_amdgcn_wave_barrier();
@@ -759,21 +816,6 @@ void launch_narrow(ConvArgs a) {
   a.tiles_n = 1;
   a.grid = (a.tiles_m + 7) / 8 * 8;
   k_conv_narrow<F16, S, T, G><<<a.grid, 256, 0, stream()>>>(a);
-}
-
-// vmcnt-only s_waitcnt (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14])
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-// Workgroup barrier without the memory fence of __syncthreads(): that fence waits for every outstanding vector
-// load (vmcnt(0)), including LDS-DMA prefetches meant to stay in flight. Callers order LDS data themselves
-// (counted vmcnt waits); the empty asm statements keep the compiler from moving memory accesses across it.
-__device__ __forceinline__ void wg_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // Wide-channel kernel, 256 sorted rows x 256 channels per workgroup (4 wavefronts, each all 256 rows x 64
@@ -1096,6 +1138,13 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   REQ((uint64_t)N * Ci * 2 <= kMaxBufferBytes && (uint64_t)Co * 27 * Ci * 2 <= kMaxBufferBytes,
       "x or w larger than %llu bytes", (unsigned long long)kMaxBufferBytes);
   a.x_bytes = (uint32_t)((uint64_t)N * Ci * 2);
+  REQ((uint64_t)N * 108 <= kMaxBufferBytes, "neighbour table larger than %llu bytes", (unsigned long long)kMaxBufferBytes);
+  a.nbr_bytes = (uint32_t)((uint64_t)N * 108);
+  if (residual) {
+    REQ((uint64_t)N * Co * dsize(residual->dt) <= kMaxBufferBytes, "residual larger than %llu bytes",
+        (unsigned long long)kMaxBufferBytes);
+    a.res_bytes = (uint32_t)((uint64_t)N * Co * dsize(residual->dt));
+  }
   a.w_bytes = (uint32_t)((uint64_t)Co * 27 * Ci * 2);
   a.N = N;
   a.Ci = Ci;
