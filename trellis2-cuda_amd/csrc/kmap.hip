@@ -17,16 +17,23 @@ namespace {
 constexpr uint32_t EMPTY = 0xffffffffu;
 constexpr uint64_t HEMPTY = ~0ull;
 
-__device__ __forceinline__ uint32_t slot_hash(uint64_t k) {
-  k ^= k >> 33;
-  k *= 0xff51afd7ed558ccdull;
-  k ^= k >> 33;
-  k *= 0xc4ceb9fe1a85ec53ull;
-  k ^= k >> 33;
-  return (uint32_t)k;
-}
 __device__ __forceinline__ uint64_t pack_key(int b, int x, int y, int z, int W, int H, int D) {
   return (((uint64_t)(uint32_t)b * (uint64_t)W + (uint64_t)x) * (uint64_t)H + (uint64_t)y) * (uint64_t)D + (uint64_t)z;
+}
+
+// Home slot of a voxel with packed key `key` and z coordinate z: the hash of its z-quad key (the key with z
+// replaced by z>>2) picks a group of 4 slots (one 64-byte line) and z&3 the slot inside it, so the z-neighbours of a
+// voxel mostly probe the same line. The quad key is folded to 32 bits and mixed with MurmurHash3's 32-bit
+// finalizer (fmix32; two 32-bit multiplies instead of 64-bit ones). Insert and probe only have to agree.
+__device__ __forceinline__ uint32_t home_slot(uint64_t key, int z, uint32_t mask) {
+  const uint64_t kq = key - (uint64_t)(z - (z >> 2));
+  uint32_t h = (uint32_t)kq ^ ((uint32_t)(kq >> 32) * 0x9e3779b1u);
+  h ^= h >> 16;
+  h *= 0x85ebca6bu;
+  h ^= h >> 13;
+  h *= 0xc2b2ae35u;
+  h ^= h >> 16;
+  return ((h << 2) | (uint32_t)(z & 3)) & mask;
 }
 
 __global__ void k_table_clear(ulonglong2* __restrict__ t, i64 cap) {
@@ -40,7 +47,7 @@ __global__ void __launch_bounds__(256) k_table_insert(const int4* __restrict__ c
   if (i >= n) return;
   int4 q = c[i];
   uint64_t k = pack_key(q.x, q.y, q.z, q.w, W, H, D);
-  for (uint32_t s = slot_hash(k) & mask;; s = (s + 1) & mask) {
+  for (uint32_t s = home_slot(k, q.w, mask);; s = (s + 1) & mask) {
     unsigned long long prev = atomicCAS((unsigned long long*)&t[s].x, (unsigned long long)HEMPTY, (unsigned long long)k);
     if (prev == HEMPTY || prev == k) {
       t[s].y = (unsigned long long)(uint32_t)i;
@@ -55,22 +62,30 @@ __global__ void __launch_bounds__(256) k_neighbors(const int4* __restrict__ c, i
                                                    uint32_t* __restrict__ nbr, int32_t* __restrict__ gray,
                                                    uint32_t* __restrict__ bin) {
   __shared__ int4 cq[NV];
+  __shared__ uint64_t ck[NV];
   __shared__ uint32_t gm[NV];
   i64 v0 = (i64)blockIdx.x * NV;
   int nv = (int)min<i64>(NV, n - v0);
   if (threadIdx.x < NV) {
     gm[threadIdx.x] = 0;
-    if ((int)threadIdx.x < nv) cq[threadIdx.x] = c[v0 + threadIdx.x];
+    if ((int)threadIdx.x < nv) {
+      const int4 q = c[v0 + threadIdx.x];
+      cq[threadIdx.x] = q;
+      ck[threadIdx.x] = pack_key(q.x, q.y, q.z, q.w, W, H, D);
+    }
   }
   __syncthreads();
+  // neighbour keys are the centre key plus a per-offset stride: key(x+dx, y+dy, z+dz) = key + (dx*H + dy)*D + dz
+  const int64_t sHD = (int64_t)H * D, sD = D;
   for (int p = threadIdx.x; p < nv * 27; p += 256) {
     int li = p / 27, v = p - li * 27;
+    const int dx = v / 9 - 1, dy = v / 3 % 3 - 1, dz = v % 3 - 1;
     int4 q = cq[li];
-    int x = q.y + v / 9 - 1, y = q.z + v / 3 % 3 - 1, z = q.w + v % 3 - 1;
+    int x = q.y + dx, y = q.z + dy, z = q.w + dz;
     uint32_t r = EMPTY;
     if (x >= 0 && x < W && y >= 0 && y < H && z >= 0 && z < D) {
-      uint64_t k = pack_key(q.x, x, y, z, W, H, D);
-      for (uint32_t s = slot_hash(k) & mask;; s = (s + 1) & mask) {
+      const uint64_t k = ck[li] + (uint64_t)(dx * sHD + dy * sD + dz);
+      for (uint32_t s = home_slot(k, z, mask);; s = (s + 1) & mask) {
         ulonglong2 e = t[s];
         if (e.x == k) {
           r = (uint32_t)e.y;
