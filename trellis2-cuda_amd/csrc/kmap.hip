@@ -4,8 +4,9 @@
 // reference, src/spconv.cu:40). Each slot is 16 bytes {u64 key, u32 row, u32 pad} so a probe is one 128-bit load
 // that returns the key and the row together (the reference keeps keys and values in two arrays, i.e. two random
 // accesses per hit). Keys pack (b,x,y,z) as ((b*W+x)*H+y)*D+z, the reference's injective packing
-// (src/spconv.cu:16,29); empty = all ones. The slot hash is MurmurHash3's 64-bit finalizer (fmix64, Austin
-// Appleby, public domain). Inserts claim a slot with a 64-bit compare-and-swap on the key.
+// (src/spconv.cu:16,29); empty = all ones. The home slot (home_slot below) hashes the voxel's z-quad with
+// MurmurHash3's 32-bit finalizer (fmix32, Austin Appleby, public domain). Inserts claim a slot with a 64-bit
+// compare-and-swap on the key.
 //
 // Neighbour map: one thread per (voxel, offset) pair, 64 voxels x 27 offsets per 256-thread workgroup, so the
 // [N,27] output is written as one contiguous, fully coalesced range per workgroup. The 27-bit mask is assembled
