@@ -58,9 +58,7 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// A zero feature row (device .bss): EMPTY neighbours gather from here, so every gather is an unconditional load.
 constexpr int kMaxCi = 8192;
-__device__ __attribute__((aligned(16))) uint16_t kZeroRow[kMaxCi];
 
 // Offset used for an EMPTY neighbour: past the end of any gathered buffer (sizes are checked to stay below it),
 // so the buffer load's range check returns zeros.
@@ -87,6 +85,10 @@ __device__ __forceinline__ void wg_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// SiLU with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each). Large negative v gives
+// exp -> inf, rcp -> 0 and a signed zero, as v / (1 + exp(-v)) does.
+__device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
 struct ConvArgs {
   const uint16_t* x;
   const uint16_t* w;
@@ -99,7 +101,7 @@ struct ConvArgs {
   const uint32_t* code;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
-  uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes;
+  uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes, out_bytes;
 };
 
 template <bool F16, int BM, int BN, int WGM, int WGN, int KC>
@@ -233,7 +235,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) k_conv(ConvArgs a) {
         if (r >= N) continue;
         i64 o = (i64)a.order[r] * a.Co + co;
         float v = acc[i][j][e] + bv;
-        if (a.act == ACT_SILU) v = v / (1.0f + expf(-v));
+        if (a.act == ACT_SILU) v = silu(v);
         if (a.res) v += load_elem(a.res, o, a.res_dt);
         store_elem(a.out, o, a.out_dt, v);
       }
@@ -252,112 +254,156 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-__device__ __forceinline__ float silu(float v) { return v * __frcp_rn(1.0f + __expf(-v)); }
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// two fp32 -> packed 16-bit, round to nearest even (bf16: one v_cvt_pk_bf16_f32)
+template <bool BF>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (BF) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+}
 
-// bias, activation, residual and one rounding for 8 consecutive output channels at element offset o
-__device__ __forceinline__ void store_row8(const ConvArgs& a, i64 o, float (&v)[8], const float (&bias8)[8]) {
-#pragma unroll
-  for (int q = 0; q < 8; q++) {
-    v[q] += bias8[q];
-    if (a.act == ACT_SILU) v[q] = silu(v[q]);
-  }
-  if (a.res) {
-    if (a.res_dt == F32) {
-      f32x4 r0 = *(const f32x4*)((const float*)a.res + o), r1 = *(const f32x4*)((const float*)a.res + o + 4);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        v[q] += r0[q];
-        v[q + 4] += r1[q];
-      }
-    } else {
-      u32x4 r = *(const u32x4*)((const uint16_t*)a.res + o);
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        uint16_t hv = (uint16_t)(r[q >> 1] >> ((q & 1) * 16));
-        v[q] += a.res_dt == BF16 ? bf16_to_f32(hv) : f16_to_f32(hv);
-      }
-    }
-  }
-  if (a.out_dt == F32) {
-    *(f32x4*)((float*)a.out + o) = f32x4{v[0], v[1], v[2], v[3]};
-    *(f32x4*)((float*)a.out + o + 4) = f32x4{v[4], v[5], v[6], v[7]};
-  } else {
-    u32x4 w;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      uint32_t lo = a.out_dt == BF16 ? f32_to_bf16(v[2 * q]) : f32_to_f16(v[2 * q]);
-      uint32_t hi = a.out_dt == BF16 ? f32_to_bf16(v[2 * q + 1]) : f32_to_f16(v[2 * q + 1]);
-      w[q] = lo | (hi << 16);
-    }
-    *(u32x4*)((uint16_t*)a.out + o) = w;
+// Epilogue target of the tiled kernels: output and residual as buffer resources. Callers pass the element offset
+// of 8 consecutive channels of one output row and whether the row exists; a missing row (past N) uses byte offset
+// kOutOfRange, so its residual loads return zeros and its stores are dropped by the range check -- no branches.
+struct Epi {
+  __amdgpu_buffer_rsrc_t out, res;
+  int out_dt, res_dt;  // res_dt < 0: no residual
+  bool silu;
+};
+__device__ __forceinline__ Epi make_epi(const ConvArgs& a) {
+  Epi e;
+  e.out = make_rsrc(a.out, a.out_bytes);
+  e.res = make_rsrc(a.res, a.res_bytes);
+  e.out_dt = a.out_dt;
+  e.res_dt = a.res ? a.res_dt : -1;
+  e.silu = a.act == ACT_SILU;
+  return e;
+}
+
+// residual segment of 8 channels as raw bits: 8 x bf16/f16 in r[0], or 8 x f32 in r[0..1]
+__device__ __forceinline__ void load_res8(const Epi& e, uint32_t o, bool ok, u32x4 (&r)[2]) {
+  r[0] = r[1] = u32x4{0, 0, 0, 0};
+  if (e.res_dt == F32) {
+    const uint32_t b = ok ? o * 4u : kOutOfRange;
+    r[0] = __builtin_amdgcn_raw_buffer_load_b128(e.res, b, 0, 0);
+    r[1] = __builtin_amdgcn_raw_buffer_load_b128(e.res, b + 16, 0, 0);
+  } else if (e.res_dt >= 0) {
+    r[0] = __builtin_amdgcn_raw_buffer_load_b128(e.res, ok ? o * 2u : kOutOfRange, 0, 0);
   }
 }
 
-// store_row8 with the residual segment already loaded (raw bits: 8 x bf16/f16 in r[0], or 8 x f32 in r[0..1])
-__device__ __forceinline__ void store_row8_pre(const ConvArgs& a, i64 o, float (&v)[8], const float (&bias8)[8],
-                                               const u32x4 (&r)[2]) {
+// out[o .. o+8) = act(v + bias) [+ residual r], one rounding to the output dtype
+__device__ __forceinline__ void store_row8(const Epi& e, uint32_t o, bool ok, float (&v)[8], const float (&bias8)[8],
+                                           const u32x4 (&r)[2]) {
 #pragma unroll
-  for (int q = 0; q < 8; q++) {
-    v[q] += bias8[q];
-    if (a.act == ACT_SILU) v[q] = silu(v[q]);
+  for (int q = 0; q < 8; q++) v[q] += bias8[q];
+  if (e.silu) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] = silu(v[q]);
   }
-  if (a.res) {
-    if (a.res_dt == F32) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        v[q] += __uint_as_float(r[0][q]);
-        v[q + 4] += __uint_as_float(r[1][q]);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        uint16_t hv = (uint16_t)(r[0][q >> 1] >> ((q & 1) * 16));
-        v[q] += a.res_dt == BF16 ? bf16_to_f32(hv) : f16_to_f32(hv);
-      }
-    }
-  }
-  if (a.out_dt == F32) {
-    *(f32x4*)((float*)a.out + o) = f32x4{v[0], v[1], v[2], v[3]};
-    *(f32x4*)((float*)a.out + o + 4) = f32x4{v[4], v[5], v[6], v[7]};
-  } else {
-    u32x4 w;
+  if (e.res_dt == F32) {
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      uint32_t lo = a.out_dt == BF16 ? f32_to_bf16(v[2 * q]) : f32_to_f16(v[2 * q]);
-      uint32_t hi = a.out_dt == BF16 ? f32_to_bf16(v[2 * q + 1]) : f32_to_f16(v[2 * q + 1]);
-      w[q] = lo | (hi << 16);
+      v[q] += __uint_as_float(r[0][q]);
+      v[q + 4] += __uint_as_float(r[1][q]);
     }
-    *(u32x4*)((uint16_t*)a.out + o) = w;
+  } else if (e.res_dt == BF16) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] += __uint_as_float((q & 1) ? (r[0][q >> 1] & 0xffff0000u) : (r[0][q >> 1] << 16));
+  } else if (e.res_dt == F16) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] += f16_to_f32((uint16_t)(r[0][q >> 1] >> ((q & 1) * 16)));
+  }
+  if (e.out_dt == F32) {
+    const uint32_t b = ok ? o * 4u : kOutOfRange;
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                                 __float_as_uint(v[3])}, e.out, b, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                                                 __float_as_uint(v[7])}, e.out, b + 16, 0, 0);
+  } else {
+    u32x4 w;
+    if (e.out_dt == BF16) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) w[q] = pack2<true>(v[2 * q], v[2 * q + 1]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++) w[q] = pack2<false>(v[2 * q], v[2 * q + 1]);
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(w, e.out, ok ? o * 2u : kOutOfRange, 0, 0);
   }
 }
 
 // Epilogue of one 32-row x 64-channel accumulator group, staged through LDS so every lane writes 16 contiguous
 // bytes: out[order[r], co] = act(acc + b) [+ residual]. `ew` is this wavefront's private [32][72] fp32 area.
+// Residual loads of one 32-row group (4 rows per lane slot p): RK 0 none, 1 fp32, 2 bf16/f16.
+template <int RK>
+__device__ __forceinline__ void load_group_res(const Epi& e, const int* tile_order, int rbase, int nrows, int Co,
+                                               int col, int lane, u32x4 (&r)[4][2]) {
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const int rr = rbase + p * 8 + (lane >> 3);
+    const uint32_t o = (uint32_t)tile_order[rr] * (uint32_t)Co + (uint32_t)col;
+    const bool ok = rr < nrows;
+    r[p][0] = r[p][1] = u32x4{0, 0, 0, 0};
+    if constexpr (RK == 1) {
+      r[p][0] = __builtin_amdgcn_raw_buffer_load_b128(e.res, ok ? o * 4u : kOutOfRange, 0, 0);
+      r[p][1] = __builtin_amdgcn_raw_buffer_load_b128(e.res, ok ? o * 4u + 16u : kOutOfRange, 0, 0);
+    } else if constexpr (RK == 2) {
+      r[p][0] = __builtin_amdgcn_raw_buffer_load_b128(e.res, ok ? o * 2u : kOutOfRange, 0, 0);
+    }
+  }
+}
+
+// Epilogue of one 32-row x 64-channel accumulator group, staged through LDS so every lane writes 16 contiguous
+// bytes: out[order[r], co] = act(acc + b) [+ residual r]. `ew` is this wavefront's private [32][72] fp32 area.
 template <int TN>
 __device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TN], float* ew, const int* tile_order, int rbase,
-                                               int nrows, int co_w, const float (&bias8)[8], const ConvArgs& a,
-                                               int lane) {
+                                               int nrows, int col, const float (&bias8)[8], const Epi& e, int Co,
+                                               int lane, const u32x4 (&r)[4][2]) {
   constexpr int ES = 72;  // row stride in floats: 4 rows apart differ by 32 banks, so the scatter is conflict-free
   const int h = lane >> 5, l32 = lane & 31;
+  const int c8 = (lane & 7) * 8;
 #pragma unroll
   for (int t = 0; t < TN; t++)
 #pragma unroll
-    for (int e = 0; e < 16; e++) ew[((e >> 2) * 8 + h * 4 + (e & 3)) * ES + t * 32 + l32] = acc[t][e];
+    for (int i = 0; i < 16; i++) ew[((i >> 2) * 8 + h * 4 + (i & 3)) * ES + t * 32 + l32] = acc[t][i];
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
-  const int c8 = (lane & 7) * 8;
 #pragma unroll
   for (int p = 0; p < 4; p++) {
     const int rr = p * 8 + (lane >> 3);
-    if (rbase + rr >= nrows) continue;
-    const i64 o = (i64)tile_order[rbase + rr] * a.Co + co_w + c8;
     float v[8];
     *(f32x4*)&v[0] = *(const f32x4*)&ew[rr * ES + c8];
     *(f32x4*)&v[4] = *(const f32x4*)&ew[rr * ES + c8 + 4];
-    store_row8(a, o, v, bias8);
+    store_row8(e, (uint32_t)tile_order[rbase + rr] * (uint32_t)Co + (uint32_t)col, rbase + rr < nrows, v, bias8, r[p]);
   }
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
+}
+
+// All TM groups of a wavefront's 32*TM x 64 accumulator tile. Stores and loads share one in-order completion
+// counter, so a residual load issued after a store cannot be waited for without also waiting for that store: the
+// residuals of group i+1 are therefore requested before the stores of group i, and a tile without a residual
+// issues no loads at all (its stores never hold the wavefront up).
+template <int TM, int TN>
+__device__ __forceinline__ void epilogue_tile(const f32x16 (&acc)[TM][TN], float* ew, const int* tile_order,
+                                              int nrows, int co_w, const float (&bias8)[8], const Epi& e, int Co,
+                                              int lane) {
+  const int col = co_w + (lane & 7) * 8;
+  auto run = [&](auto RKc) __attribute__((always_inline)) {
+    constexpr int RK = decltype(RKc)::value;
+    u32x4 r[2][4][2];
+    load_group_res<RK>(e, tile_order, 0, nrows, Co, col, lane, r[0]);
+    static_for<TM>([&](auto I) __attribute__((always_inline)) {
+      if constexpr (I + 1 < TM) load_group_res<RK>(e, tile_order, (I + 1) * 32, nrows, Co, col, lane, r[(I + 1) & 1]);
+      epilogue_group<TN>(acc[I], ew, tile_order, I * 32, nrows, col, bias8, e, Co, lane, r[I & 1]);
+    });
+  };
+  if (e.res_dt < 0) run(std::integral_constant<int, 0>{});
+  else if (e.res_dt == F32) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 2>{});
 }
 
 // Wide-channel kernel: BM sorted rows x BN = 64*NW channels, NW wavefronts; each wavefront owns all BM rows x its
@@ -372,7 +418,7 @@ __device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TN], float* e
 //  * Only A is shared by the wavefronts, so only A goes through LDS; weights (L2-resident) stream straight into
 //    MFMA operand registers. At tile start the offset list, the 32-row masks, the tile's output row indices and its
 //    [BM x 27] neighbour indices are staged in LDS: the K loop has no dependent global loads. EMPTY neighbours
-//    gather from a zero row in device memory, so every gather is an unconditional 16-byte load.
+//    read past the end of the feature buffer, so every gather is an unconditional 16-byte load.
 //  * LDS layout of a stage: row r occupies 128 contiguous bytes as eight 16-byte slots; channel piece p of row r is
 //    stored in slot p ^ (r & 7) so the MFMA operand reads (32 rows, one piece) hit distinct banks.
 //  * Within a 64-channel stage the K order is permuted (lane half h, step j -> piece h*4 + j) identically for A and
@@ -559,7 +605,8 @@ __global__ void __launch_bounds__(NW * 64) k_conv_wide(ConvArgs a) {
 #pragma unroll
   for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[co_w + (lane & 7) * 8 + q] : 0.f;
   const int nrows = N - row0;
-  static_for<TM>([&](auto I) { epilogue_group<TN>(acc[I], ew, ordT, I * 32, nrows, co_w, bias8, a, lane); });
+  const Epi e = make_epi(a);
+  epilogue_tile<TM, TN>(acc, ew, ordT, nrows, co_w, bias8, e, a.Co, lane);
 }
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
@@ -767,6 +814,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 #pragma unroll
   for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[c8 + q] : 0.f;
   constexpr int NP = 16 / RPP;
+  const Epi e = make_epi(a);
   u32x4 resv[G][NP][2];
   if (a.res && !res16) {  // fp32 residual: straight to registers, all requested before the first group
 #pragma unroll
@@ -774,10 +822,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 #pragma unroll
       for (int p = 0; p < NP; p++) {
         const int lrow = wv * (16 * G) + i * 16 + p * RPP + lane / LPR;
-        const i64 o = (i64)ordT[lrow] * CO + c8;
-        const bool ok = row0 + lrow < N;
-        resv[i][p][0] = ok ? *(const u32x4*)((const float*)a.res + o) : u32x4{0, 0, 0, 0};
-        resv[i][p][1] = ok ? *(const u32x4*)((const float*)a.res + o + 4) : u32x4{0, 0, 0, 0};
+        load_res8(e, (uint32_t)ordT[lrow] * CO + c8, row0 + lrow < N, resv[i][p]);
       }
   }
   if (res16) {
@@ -789,20 +834,18 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 #pragma unroll
     for (int t = 0; t < T; t++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) ew[(q4 * 4 + e) * ES + t * 16 + r16] = acc[i][t][e];
+      for (int q = 0; q < 4; q++) ew[(q4 * 4 + q) * ES + t * 16 + r16] = acc[i][t][q];
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int p = 0; p < NP; p++) {
       const int rr = p * RPP + lane / LPR;
       const int lrow = wv * (16 * G) + i * 16 + rr;
-      if (row0 + lrow >= N) continue;
-      const i64 o = (i64)ordT[lrow] * CO + c8;
       float v8[8];
       *(f32x4*)&v8[0] = *(const f32x4*)&ew[rr * ES + c8];
       *(f32x4*)&v8[4] = *(const f32x4*)&ew[rr * ES + c8 + 4];
       if (res16) resv[i][p][0] = resL[lrow * LPR + lane % LPR];
-      store_row8_pre(a, o, v8, bias8, resv[i][p]);
+      store_row8(e, (uint32_t)ordT[lrow] * CO + c8, row0 + lrow < N, v8, bias8, resv[i][p]);
     }
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
@@ -1006,7 +1049,8 @@ __global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
 #pragma unroll
   for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[co_w + (lane & 7) * 8 + q] : 0.f;
   const int nrows = N - row0;
-  static_for<TM>([&](auto I) { epilogue_group<TN>(acc[I], ew, ordT, I * 32, nrows, co_w, bias8, a, lane); });
+  const Epi e = make_epi(a);
+  epilogue_tile<TM, TN>(acc, ew, ordT, nrows, co_w, bias8, e, a.Co, lane);
 }
 
 template <bool F16>
@@ -1145,6 +1189,9 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
         (unsigned long long)kMaxBufferBytes);
     a.res_bytes = (uint32_t)((uint64_t)N * Co * dsize(residual->dt));
   }
+  REQ((uint64_t)N * Co * dsize(out.dt) <= kMaxBufferBytes, "output larger than %llu bytes",
+      (unsigned long long)kMaxBufferBytes);
+  a.out_bytes = (uint32_t)((uint64_t)N * Co * dsize(out.dt));
   a.w_bytes = (uint32_t)((uint64_t)Co * 27 * Ci * 2);
   a.N = N;
   a.Ci = Ci;
