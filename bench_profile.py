@@ -16,6 +16,7 @@ import csv
 import glob
 import json
 import os
+import re
 import subprocess
 import sys
 
@@ -53,6 +54,8 @@ def main():
     ap.add_argument("--config", default="c3")
     ap.add_argument("--out", default=os.path.join(ROOT, "gpurun_out", "prof"))
     ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--profiles-dir", default=os.path.join(ROOT, "profiles"),
+                    help="where the summary and traffic_<config>.json go (on a GPU box: somewhere that is copied back)")
     args = ap.parse_args()
     out = os.path.join(args.out, args.config)
     os.makedirs(out, exist_ok=True)
@@ -67,7 +70,8 @@ def main():
     stats.sort(key=lambda r: -float(r["TotalDurationNs"]))
     top = stats[0]
     kname = top["Name"]
-    key = "k_conv_wide" if "k_conv_wide" in kname else ("k_conv_narrow" if "k_conv_narrow" in kname else "k_conv")
+    m = re.search(r"(k_conv\w*)", kname)  # the kernel's base name, e.g. k_conv_wide_dma
+    key = m.group(1) if m else "k_conv"
     figs = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         run(rp + ["--pmc", counter, "-d", f"{out}/{counter}", "--"] + bench, 300, f"{out}/{counter}.log")
@@ -83,7 +87,7 @@ def main():
            "copy_fetch_KiB": figs["copy_FETCH_SIZE"][0], "copy_write_KiB": figs["copy_WRITE_SIZE"][0],
            "copy_bytes": COPY_BYTES, "fetch_factor": fetch_factor, "write_factor": write_factor,
            "traffic_bytes": fetch_b + write_b}
-    prof = os.path.join(ROOT, "profiles")
+    prof = args.profiles_dir
     os.makedirs(prof, exist_ok=True)
     with open(os.path.join(prof, f"traffic_{args.config}.json"), "w") as f:
         json.dump(res, f, indent=1)

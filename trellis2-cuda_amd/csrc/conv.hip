@@ -1203,7 +1203,7 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
-    a.order = c.window_order(12).ptr<int32_t>();
+    a.order = c.window_order(16).ptr<int32_t>();
   } else if (cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
