@@ -97,11 +97,13 @@ struct ConvArgs {
   void* out;
   const uint32_t* nbr;
   const int32_t* order;
+  const uint32_t* tbl;  // neighbour table in tile order (SpConvCache::row_table), for the kernels that use it
+  const int32_t* gs;    // neighbour masks in tile order
   const int32_t* gray;
   const uint32_t* code;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
-  uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes, out_bytes;
+  uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes, out_bytes, tbl_bytes;
 };
 
 template <bool F16, int BM, int BN, int WGM, int WGN, int KC>
@@ -649,12 +651,32 @@ __global__ void k_pack_w_narrow(const u32x4* __restrict__ w, u32x4* __restrict__
 //    MFMAs for it. Rows come in the order the caller chooses (null = identity); the spatial (Morton) order keeps
 //    the gathers of neighbouring rows in L2.
 //  * Epilogue: per 16-row group, accumulators go through LDS and leave as 16-byte segments of whole output rows.
+// Copies rows [row0, row0+BM) of the tile-ordered neighbour table (27 u32 per row, contiguous) into LDS by DMA:
+// 16 bytes per lane, so each wavefront instruction moves 1 KiB with no registers involved.
+template <int BM, int NT>
+__device__ __forceinline__ void dma_tile_table(const ConvArgs& a, int row0, uint32_t* srcT, int tid) {
+  constexpr int TU = BM * 27 / 4;  // 16-byte units
+  const __amdgpu_buffer_rsrc_t rt = make_rsrc(a.tbl, a.tbl_bytes);
+  const uint32_t base = (uint32_t)row0 * 108u;
+#pragma unroll
+  for (int k = 0; k < (TU + NT - 1) / NT; k++) {
+    const int u = k * NT + tid;
+    if (u < TU)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)&srcT[(k * NT + (tid & ~63)) * 4],
+                                               16, base + (uint32_t)u * 16u, 0, 0, 0);
+  }
+}
+// Byte offset of neighbour row n in a feature matrix with `rowbytes` bytes per row; EMPTY -> past the buffer end
+__device__ __forceinline__ uint32_t nbr_offset(uint32_t n, uint32_t rowbytes) {
+  return n == EMPTY ? kOutOfRange : n * rowbytes;
+}
+
 template <bool F16, int S, int T, int G>
 __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   constexpr int NT = 256, BM = 4 * 16 * G, CI = 32 * S, CO = 16 * T, WB = T * S * 64;  // WB: 16B units per offset
   static_assert(WB % NT == 0, "weight slice split");
   __shared__ __attribute__((aligned(16))) u32x4 Bs[2][WB];
-  constexpr int SR = 28;  // srcT row stride: 27 offsets padded to 7 x 16 bytes
+  constexpr int SR = 27;  // srcT row stride: the table's 27 neighbour indices per row
   __shared__ __attribute__((aligned(16))) uint32_t srcT[BM * SR];
   __shared__ int ordT[BM];
   __shared__ __attribute__((aligned(16))) u32x4 resL[BM * CO * 2 / 16];
@@ -668,41 +690,18 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
   const int N = a.N;
 
-  if (tid < BM) {  // prologue: rows, 16-row masks, offset list, neighbour byte offsets
+  // prologue: the tile's block of the neighbour table goes to LDS by DMA; rows, 16-row masks from the same order
+  dma_tile_table<BM, NT>(a, row0, srcT, tid);
+  if (tid < BM) {
     const int row = row0 + tid;
     const bool live = row < N;
-    const int o = live ? (a.order ? a.order[row] : row) : 0;
-    ordT[tid] = o;
-    // the row's 27 neighbour indices: one contiguous 108-byte run, fetched as 6 x 16 + 12 bytes
-    const __amdgpu_buffer_rsrc_t rn = make_rsrc(a.nbr, a.nbr_bytes);
-    uint32_t src[28];
-#pragma unroll
-    for (int j = 0; j < 6; j++) {
-      const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rn, (uint32_t)o * 108u + j * 16, 0, 0);
-#pragma unroll
-      for (int e = 0; e < 4; e++) src[j * 4 + e] = q[e];
-    }
-    {
-      const u32x3 q = __builtin_amdgcn_raw_buffer_load_b96(rn, (uint32_t)o * 108u + 96, 0, 0);
-      src[24] = q[0];
-      src[25] = q[1];
-      src[26] = q[2];
-      src[27] = EMPTY;
-    }
-    uint32_t gm = 0;  // the row's neighbour mask, straight from its table row
-#pragma unroll
-    for (int v = 0; v < 28; v++) {
-      const bool e = !live || src[v] == EMPTY;
-      if (v < 27) gm |= e ? 0u : 1u << v;
-      src[v] = e ? kOutOfRange : src[v] * (uint32_t)(CI * 2);
-    }
-#pragma unroll
-    for (int j = 0; j < 7; j++)
-      *(u32x4*)&srcT[tid * SR + j * 4] = u32x4{src[j * 4], src[j * 4 + 1], src[j * 4 + 2], src[j * 4 + 3]};
+    ordT[tid] = live ? a.order[row] : 0;
+    uint32_t gm = a.gs[row];  // padded rows have mask 0
 #pragma unroll
     for (int d = 1; d < 16; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
     if ((tid & 15) == 0) gmask[tid >> 4] = gm;
   }
+  wait_vmcnt<0>();  // this lane's table DMA has landed (the barrier below covers the other lanes)
   __syncthreads();
   uint32_t mask = 0;
 #pragma unroll
@@ -726,7 +725,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
     const int v = __builtin_amdgcn_readfirstlane(vlist[vi]);
     uint32_t off[G];  // all groups' row offsets first: one LDS round trip, not one per group
 #pragma unroll
-    for (int i = 0; i < G; i++) off[i] = srcT[(wv * (16 * G) + i * 16 + r16) * SR + v] + q4 * (S * 16);
+    for (int i = 0; i < G; i++) off[i] = nbr_offset(srcT[(wv * (16 * G) + i * 16 + r16) * SR + v], CI * 2) + q4 * (S * 16);
 #pragma unroll
     for (int i = 0; i < G; i++) {
       if ((gms[i] >> v) & 1u) {
@@ -781,25 +780,30 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   }
   __syncthreads();  // vlist visible
   if (nvv > 0) {
-    u32x4 rb0[BL], rb1[BL];
+    u32x4 rb[2][BL];
     {
       const int v0 = __builtin_amdgcn_readfirstlane(vlist[0]);
       const int v1 = __builtin_amdgcn_readfirstlane(vlist[nvv > 1 ? 1 : 0]);
 #pragma unroll
       for (int k = 0; k < BL; k++) Bs[0][k * NT + tid] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, v0 * WB * 16, 0);
 #pragma unroll
-      for (int k = 0; k < BL; k++) rb1[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, v1 * WB * 16, 0);
+      for (int k = 0; k < BL; k++) rb[1][k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, v1 * WB * 16, 0);
     }
-    u32x4 ra0[G][S], ra1[G][S];
-    gather(0, ra0);
+    u32x4 ra[3][G][S];
+    gather(0, ra[0]);
+    if (nvv > 1) gather(1, ra[1]);
     __syncthreads();
-    // software pipeline: gathers of entry vi+1 and weights of entry vi+2 are in flight while entry vi computes
-    for (int vi = 0; vi < nvv; vi += 2) {
-      if (vi + 1 < nvv) gather(vi + 1, ra1);
-      compute(vi, 0, ra0, rb0, rb1);
-      if (vi + 1 >= nvv) break;
-      if (vi + 2 < nvv) gather(vi + 2, ra0);
-      compute(vi + 1, 1, ra1, rb1, rb0);
+    // software pipeline: gathers of entries vi+1 and vi+2 and the weights of entry vi+2 are in flight while entry vi
+    // computes (gather buffers rotate by 3, weight buffers by 2: unrolled by 6 so every buffer has a fixed name)
+    for (int vb = 0; vb < nvv; vb += 6) {
+      static_for<6>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        const int vi = vb + j;
+        if (vi < nvv) {
+          if (vi + 2 < nvv) gather(vi + 2, ra[(j + 2) % 3]);
+          compute(vi, j & 1, ra[j % 3], rb[j & 1], rb[(j + 1) & 1]);
+        }
+      });
     }
   }
 
@@ -889,24 +893,17 @@ __global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
   const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int N = a.N, Ci = a.Ci, nkc = Ci / KC;
 
-  {  // prologue: row indices, 32-row masks, neighbour byte offsets (one row per thread)
+  // prologue: the tile's block of the neighbour table goes to LDS by DMA; rows and 32-row masks from the same order
+  dma_tile_table<BM, NT>(a, row0, srcT, tid);
+  {
     const int row = row0 + tid;
-    const int o = row < N ? a.order[row] : 0;
-    ordT[tid] = o;
-    uint32_t src[27];
-    const uint32_t* nrow = a.nbr + (i64)o * 27;
-#pragma unroll
-    for (int v = 0; v < 27; v++) src[v] = row < N ? nrow[v] : EMPTY;
-    uint32_t gm = 0;
-#pragma unroll
-    for (int v = 0; v < 27; v++) {
-      gm |= src[v] == EMPTY ? 0u : 1u << v;
-      srcT[tid * 27 + v] = src[v] == EMPTY ? kOutOfRange : src[v] * (uint32_t)(Ci * 2);
-    }
+    ordT[tid] = row < N ? a.order[row] : 0;
+    uint32_t gm = a.gs[row];  // padded rows have mask 0
 #pragma unroll
     for (int d = 1; d < 32; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
     if ((tid & 31) == 0) gmask[tid >> 5] = gm;
   }
+  wait_vmcnt<0>();  // this lane's table DMA has landed (the barrier below covers the other lanes)
   __syncthreads();
   uint32_t mask = 0;
 #pragma unroll
@@ -944,7 +941,7 @@ __global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
     ka = __builtin_amdgcn_readfirstlane((live ? akc : nkc - 1) * KC * 2);
     next(avi, akc);
 #pragma unroll
-    for (int k = 0; k < AL; k++) off[k] = srcT[drow[k] * 27 + va] + dpiece[k] * 16;
+    for (int k = 0; k < AL; k++) off[k] = nbr_offset(srcT[drow[k] * 27 + va], (uint32_t)(Ci * 2)) + dpiece[k] * 16;
   };
   auto dma = [&](u32x4* slot, int k, uint32_t off, int ka) __attribute__((always_inline)) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)&slot[(wn * AL + k) * 64],
@@ -1182,7 +1179,8 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   REQ((uint64_t)N * Ci * 2 <= kMaxBufferBytes && (uint64_t)Co * 27 * Ci * 2 <= kMaxBufferBytes,
       "x or w larger than %llu bytes", (unsigned long long)kMaxBufferBytes);
   a.x_bytes = (uint32_t)((uint64_t)N * Ci * 2);
-  REQ((uint64_t)N * 108 <= kMaxBufferBytes, "neighbour table larger than %llu bytes", (unsigned long long)kMaxBufferBytes);
+  REQ(((uint64_t)N + SpConvCache::kRowTablePad) * 108 <= kMaxBufferBytes, "neighbour table larger than %llu bytes",
+      (unsigned long long)kMaxBufferBytes);
   a.nbr_bytes = (uint32_t)((uint64_t)N * 108);
   if (residual) {
     REQ((uint64_t)N * Co * dsize(residual->dt) <= kMaxBufferBytes, "residual larger than %llu bytes",
@@ -1203,11 +1201,21 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
-    a.order = c.window_order(16).ptr<int32_t>();
+    const SpConvCache::RowTable& rt = c.row_table(16);
+    a.order = rt.order.ptr<int32_t>();
+    a.tbl = rt.tbl.ptr<uint32_t>();
+    a.gs = rt.gs.ptr<int32_t>();
+    a.tbl_bytes = (uint32_t)rt.tbl.bytes();
   } else if (cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
+    if (Co % 256 == 0) {  // the 256 x 256 kernel reads its tiles' neighbour rows from the sorted-order table
+      const SpConvCache::RowTable& rt = c.row_table(-1);
+      a.tbl = rt.tbl.ptr<uint32_t>();
+      a.gs = rt.gs.ptr<int32_t>();
+      a.tbl_bytes = (uint32_t)rt.tbl.bytes();
+    }
   }
   if (x.dt == F16) dispatch<true>(cfg, a);
   else dispatch<false>(cfg, a);

@@ -235,6 +235,36 @@ const Tensor& SpConvCache::window_order(int log2w) {
   return worder.emplace(log2w, o).first->second;
 }
 
+// tbl[i][v] = nbr[order[i]][v], gs[i] = gray[order[i]]; rows past n are EMPTY with a zero mask. One thread per
+// (row, offset) pair, so both the 108-byte source rows and the table are read and written contiguously.
+__global__ void k_row_table(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ gray,
+                            const int32_t* __restrict__ order, i64 n, i64 npad, uint32_t* __restrict__ tbl,
+                            int32_t* __restrict__ gs) {
+  const i64 p = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= npad * 27) return;
+  const i64 i = p / 27;
+  const int v = (int)(p - i * 27);
+  const int o = i < n ? order[i] : 0;
+  tbl[p] = i < n ? nbr[(i64)o * 27 + v] : EMPTY;
+  if (v == 0) gs[i] = i < n ? gray[o] : 0;
+}
+
+const SpConvCache::RowTable& SpConvCache::row_table(int log2w) {
+  const int key = log2w < 0 ? -1 : log2w;
+  auto it = rtab.find(key);
+  if (it != rtab.end()) return it->second;
+  RowTable r;
+  r.order = key < 0 ? sorted : window_order(key);
+  const i64 npad = std::max<i64>(cdiv(N, kRowTablePad), 1) * kRowTablePad;
+  r.tbl = empty({npad, 27}, I32);
+  r.gs = empty({npad}, I32);
+  k_row_table<<<cdiv(npad * 27, 256), 256, 0, stream()>>>(nbr.ptr<uint32_t>(), gray.ptr<int32_t>(),
+                                                          r.order.ptr<int32_t>(), N, npad, r.tbl.ptr<uint32_t>(),
+                                                          r.gs.ptr<int32_t>());
+  CK(hipGetLastError());
+  return rtab.emplace(key, r).first->second;
+}
+
 const std::pair<Tensor, Tensor>& SpConvCache::valid(int B1) {
   auto it = vk.find(B1);
   if (it != vk.end()) return it->second;

@@ -26,6 +26,16 @@ struct SpConvCache {
   // gathers stay spatially close. Used by the narrow-channel kernels.
   std::map<int, Tensor> worder;
   const Tensor& window_order(int log2w);
+  // The neighbour table in a tile order, so a conv tile reads its rows' neighbour indices as one contiguous block:
+  // tbl[i] = nbr[order[i]] (27 u32, EMPTY kept) and gs[i] = gray[order[i]], padded with EMPTY rows and zero masks
+  // to a multiple of kRowTablePad rows; order = window_order(log2w), or sorted for log2w < 0. Memoized, like the
+  // schedules above: a decoder runs many convs on one cache.
+  static constexpr int kRowTablePad = 256;
+  struct RowTable {
+    Tensor order, tbl, gs;
+  };
+  std::map<int, RowTable> rtab;
+  const RowTable& row_table(int log2w);
 };
 SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D);  // coords int32 [N,4] (b,x,y,z)
 
