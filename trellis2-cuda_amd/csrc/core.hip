@@ -1,6 +1,7 @@
 #include "core.h"
 
 #include <cstdarg>
+#include <mutex>
 #include <stdexcept>
 
 void spc_fail(const char* fmt, ...) {
@@ -34,18 +35,73 @@ Tensor borrow(const void* p, std::vector<i64> sh, DT dt) {
   return t;
 }
 
+// Device memory: a caching allocator over hipMallocAsync. hipFreeAsync costs tens of microseconds of host time per
+// call on this platform, and a kernel-map build allocates a dozen temporaries, so freed blocks are kept in per
+// (device, stream, size class) free lists and handed out again. Reuse is stream-ordered: a block freed while
+// kernels on its stream may still use it is only ever reissued to later work on that same stream. Size classes:
+// powers of two up to 1 MiB, then multiples of 2 MiB. Cached blocks are kept until the process ends (like a
+// framework's caching allocator); the pool's release threshold is raised too, so blocks that do go back to the
+// driver stay mapped.
+namespace {
+struct BlockKey {
+  int dev;
+  hipStream_t stream;
+  size_t size;
+  bool operator<(const BlockKey& o) const {
+    if (dev != o.dev) return dev < o.dev;
+    if (stream != o.stream) return stream < o.stream;
+    return size < o.size;
+  }
+};
+std::mutex g_alloc_mu;
+std::map<BlockKey, std::vector<void*>>& free_blocks() {
+  static auto* m = new std::map<BlockKey, std::vector<void*>>();  // never destroyed: frees can run at exit
+  return *m;
+}
+size_t size_class(size_t n) {
+  if (n <= (1u << 20)) {
+    size_t c = 512;
+    while (c < n) c <<= 1;
+    return c;
+  }
+  const size_t g = 2u << 20;
+  return (n + g - 1) / g * g;
+}
+void keep_pool_memory(int dev) {
+  static bool done[64] = {};
+  if (dev < 0 || dev >= 64 || done[dev]) return;
+  hipMemPool_t pool;
+  CK(hipDeviceGetDefaultMemPool(&pool, dev));
+  uint64_t keep = UINT64_MAX;
+  CK(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep));
+  done[dev] = true;
+}
+}  // namespace
+
 Tensor empty(std::vector<i64> sh, DT dt) {
   Tensor t;
   t.sh = std::move(sh);
   t.dt = dt;
-  size_t n = (t.bytes() + 16 + 511) & ~size_t(511);
   if (t.bytes()) {
+    int dev = 0;
+    CK(hipGetDevice(&dev));
+    const BlockKey key{dev, stream(), size_class(t.bytes() + 16)};
     void* p = nullptr;
-    hipStream_t s = stream();
-    CK(hipMallocAsync(&p, n, s));
+    {
+      std::lock_guard<std::mutex> g(g_alloc_mu);
+      keep_pool_memory(dev);
+      auto& fl = free_blocks()[key];
+      if (!fl.empty()) {
+        p = fl.back();
+        fl.pop_back();
+      }
+    }
+    if (!p) CK(hipMallocAsync(&p, key.size, key.stream));
     t.p = p;
-    // frees are ordered on the stream the tensor was allocated on
-    t.own = std::shared_ptr<void>(p, [s](void* q) { (void)hipFreeAsync(q, s); });
+    t.own = std::shared_ptr<void>(p, [key](void* q) {
+      std::lock_guard<std::mutex> g(g_alloc_mu);
+      free_blocks()[key].push_back(q);
+    });
   }
   return t;
 }

@@ -1,12 +1,13 @@
 // Voxel hash table + 27-offset kernel map + block schedules (reference src/spconv.cu:10-75).
 //
-// Hash table: open addressing with linear probing, capacity = next pow2 >= 2N (load factor <= 0.5, as the
-// reference, src/spconv.cu:40). Each slot is 16 bytes {u64 key, u32 row, u32 pad} so a probe is one 128-bit load
-// that returns the key and the row together (the reference keeps keys and values in two arrays, i.e. two random
-// accesses per hit). Keys pack (b,x,y,z) as ((b*W+x)*H+y)*D+z, the reference's injective packing
-// (src/spconv.cu:16,29); empty = all ones. The home slot (home_slot below) hashes the voxel's z-quad with
-// MurmurHash3's 32-bit finalizer (fmix32, Austin Appleby, public domain). Inserts claim a slot with a 64-bit
-// compare-and-swap on the key.
+// The reference answers each of the 27 neighbour queries of a voxel with a probe of a voxel-keyed hash table
+// (src/spconv.cu:13-36). Only the answers are observable (nbr rows, masks, the sorted order; bit-exact here), so
+// the lookup structure is this build's own: a brick table. Space is cut into 4x4x4-voxel bricks; an
+// open-addressed table (linear probing, capacity = next pow2 >= 2N, so it never fills even if every voxel is its
+// own brick) maps the packed 64-bit brick key ((b*W4+x/4)*H4+y/4)*D4+z/4 to the brick's record of 64 rows.
+// Slots are 16 bytes {u64 key, u32 id, pad}: one 128-bit load returns key and id together. Inserts claim a slot
+// with a 64-bit compare-and-swap; the slot hash is MurmurHash3's 32-bit finalizer (fmix32, Austin Appleby, public
+// domain) of the folded key.
 //
 // Neighbour map: one thread per (voxel, offset) pair, 64 voxels x 27 offsets per 256-thread workgroup, so the
 // [N,27] output is written as one contiguous, fully coalesced range per workgroup. The 27-bit mask is assembled
@@ -18,82 +19,110 @@ namespace {
 constexpr uint32_t EMPTY = 0xffffffffu;
 constexpr uint64_t HEMPTY = ~0ull;
 
-__device__ __forceinline__ uint64_t pack_key(int b, int x, int y, int z, int W, int H, int D) {
-  return (((uint64_t)(uint32_t)b * (uint64_t)W + (uint64_t)x) * (uint64_t)H + (uint64_t)y) * (uint64_t)D + (uint64_t)z;
-}
-
-// Home slot of a voxel with packed key `key` and z coordinate z: the hash of its z-quad key (the key with z
-// replaced by z>>2) picks a group of 4 slots (one 64-byte line) and z&3 the slot inside it, so the z-neighbours of a
-// voxel mostly probe the same line. The quad key is folded to 32 bits and mixed with MurmurHash3's 32-bit
-// finalizer (fmix32; two 32-bit multiplies instead of 64-bit ones). Insert and probe only have to agree.
-__device__ __forceinline__ uint32_t home_slot(uint64_t key, int z, uint32_t mask) {
-  const uint64_t kq = key - (uint64_t)(z - (z >> 2));
-  uint32_t h = (uint32_t)kq ^ ((uint32_t)(kq >> 32) * 0x9e3779b1u);
-  h ^= h >> 16;
-  h *= 0x85ebca6bu;
-  h ^= h >> 13;
-  h *= 0xc2b2ae35u;
-  h ^= h >> 16;
-  return ((h << 2) | (uint32_t)(z & 3)) & mask;
-}
-
 __global__ void k_table_clear(ulonglong2* __restrict__ t, i64 cap) {
   i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < cap) t[i] = make_ulonglong2(HEMPTY, HEMPTY);
 }
 
-__global__ void __launch_bounds__(256) k_table_insert(const int4* __restrict__ c, i64 n, int W, int H, int D,
-                                                      ulonglong2* __restrict__ t, uint32_t mask) {
-  i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  int4 q = c[i];
-  uint64_t k = pack_key(q.x, q.y, q.z, q.w, W, H, D);
-  for (uint32_t s = home_slot(k, q.w, mask);; s = (s + 1) & mask) {
-    unsigned long long prev = atomicCAS((unsigned long long*)&t[s].x, (unsigned long long)HEMPTY, (unsigned long long)k);
-    if (prev == HEMPTY || prev == k) {
-      t[s].y = (unsigned long long)(uint32_t)i;
-      return;
-    }
+constexpr int NV = 64;  // voxels per workgroup in the neighbour kernel
+
+// ------------------------------------------------------------------------------------------ brick table
+// Exact lookup structure for the neighbour query (only its answers are observable: nbr rows are bit-exact whatever
+// the structure). Space is cut into bricks of 4x4x4 voxels; an open-addressed table keyed by the packed brick
+// coordinate (b, x>>2, y>>2, z>>2) maps each occupied brick to a dense id, and bricks[id*64 + local] holds the
+// row of every voxel in it (EMPTY elsewhere). The 27 neighbours of a voxel fall in 1-8 bricks (3.4 on average),
+// so a voxel's probes touch a few table lines instead of one per neighbour column, and the rows it reads sit in
+// a few 256-byte brick records shared with the voxels around it.
+__device__ __forceinline__ uint64_t brick_key(int b, int x, int y, int z, int W4, int H4, int D4) {
+  return (((uint64_t)(uint32_t)b * (uint64_t)W4 + (uint64_t)(x >> 2)) * (uint64_t)H4 + (uint64_t)(y >> 2)) *
+             (uint64_t)D4 + (uint64_t)(z >> 2);
+}
+__device__ __forceinline__ int brick_local(int x, int y, int z) { return ((x & 3) << 4) | ((y & 3) << 2) | (z & 3); }
+__device__ __forceinline__ uint32_t brick_home(uint64_t k, uint32_t mask) {
+  uint32_t h = (uint32_t)k ^ ((uint32_t)(k >> 32) * 0x9e3779b1u);
+  h ^= h >> 16;
+  h *= 0x85ebca6bu;
+  h ^= h >> 13;
+  h *= 0xc2b2ae35u;
+  h ^= h >> 16;
+  return h & mask;
+}
+// Probe for brick key k: its id, or EMPTY when the brick holds no voxel.
+__device__ __forceinline__ uint32_t brick_find(const ulonglong2* __restrict__ t, uint64_t k, uint32_t mask) {
+  for (uint32_t s = brick_home(k, mask);; s = (s + 1) & mask) {
+    const ulonglong2 e = t[s];
+    if (e.x == k) return (uint32_t)e.y;
+    if (e.x == HEMPTY) return EMPTY;
   }
 }
 
-constexpr int NV = 64;  // voxels per workgroup in the neighbour kernel
-__global__ void __launch_bounds__(256) k_neighbors(const int4* __restrict__ c, i64 n, int W, int H, int D,
-                                                   const ulonglong2* __restrict__ t, uint32_t mask,
-                                                   uint32_t* __restrict__ nbr, int32_t* __restrict__ gray,
-                                                   uint32_t* __restrict__ bin) {
+// Claims a slot for every occupied brick. A brick's id is the row of the voxel that inserted it (unique, so no
+// shared counter), and that thread clears the brick's 64-entry record.
+__global__ void __launch_bounds__(256) k_brick_insert(const int4* __restrict__ c, i64 n, int W4, int H4, int D4,
+                                                      ulonglong2* __restrict__ t, uint32_t mask,
+                                                      uint4* __restrict__ bricks) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t k = HEMPTY;
+  if (i < n) {
+    const int4 q = c[i];
+    k = brick_key(q.x, q.y, q.z, q.w, W4, H4, D4);
+  }
+  // Voxels of one brick are usually adjacent rows (spatially sorted input): only the first lane of a run of equal
+  // keys inserts, so a brick sees one compare-and-swap instead of one per voxel. (Other duplicates stay correct:
+  // the compare-and-swap finds the key.)
+  const int lane = threadIdx.x & 63;
+  const uint64_t kprev = ((uint64_t)(uint32_t)__shfl_up((int)(uint32_t)(k >> 32), 1, 64) << 32) |
+                         (uint32_t)__shfl_up((int)(uint32_t)k, 1, 64);
+  if (i >= n || (lane != 0 && kprev == k)) return;
+  for (uint32_t s = brick_home(k, mask);; s = (s + 1) & mask) {
+    const unsigned long long prev =
+        atomicCAS((unsigned long long*)&t[s].x, (unsigned long long)HEMPTY, (unsigned long long)k);
+    if (prev == HEMPTY) {
+      t[s].y = (unsigned long long)i;
+#pragma unroll
+      for (int u = 0; u < 16; u++) bricks[i * 16 + u] = make_uint4(EMPTY, EMPTY, EMPTY, EMPTY);
+      return;
+    }
+    if (prev == k) return;
+  }
+}
+
+__global__ void __launch_bounds__(256) k_brick_fill(const int4* __restrict__ c, i64 n, int W4, int H4, int D4,
+                                                    const ulonglong2* __restrict__ t, uint32_t mask,
+                                                    uint32_t* __restrict__ bricks) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int4 q = c[i];
+  const uint32_t id = brick_find(t, brick_key(q.x, q.y, q.z, q.w, W4, H4, D4), mask);
+  bricks[(i64)id * 64 + brick_local(q.y, q.z, q.w)] = (uint32_t)i;
+}
+
+// 64 voxels x 27 offsets per workgroup, one thread per (voxel, offset) pair, so the [N,27] output is one contiguous,
+// fully coalesced range per workgroup; the 27-bit mask is assembled with LDS atomic OR and decoded
+// (gray -> binary prefix xor) by one thread per voxel.
+__global__ void __launch_bounds__(256) k_neighbors_brick(const int4* __restrict__ c, i64 n, int W, int H, int D,
+                                                         const ulonglong2* __restrict__ t, uint32_t mask,
+                                                         const uint32_t* __restrict__ bricks,
+                                                         uint32_t* __restrict__ nbr, int32_t* __restrict__ gray,
+                                                         uint32_t* __restrict__ bin) {
   __shared__ int4 cq[NV];
-  __shared__ uint64_t ck[NV];
   __shared__ uint32_t gm[NV];
-  i64 v0 = (i64)blockIdx.x * NV;
-  int nv = (int)min<i64>(NV, n - v0);
+  const i64 v0 = (i64)blockIdx.x * NV;
+  const int nv = (int)min<i64>(NV, n - v0);
   if (threadIdx.x < NV) {
     gm[threadIdx.x] = 0;
-    if ((int)threadIdx.x < nv) {
-      const int4 q = c[v0 + threadIdx.x];
-      cq[threadIdx.x] = q;
-      ck[threadIdx.x] = pack_key(q.x, q.y, q.z, q.w, W, H, D);
-    }
+    if ((int)threadIdx.x < nv) cq[threadIdx.x] = c[v0 + threadIdx.x];
   }
   __syncthreads();
-  // neighbour keys are the centre key plus a per-offset stride: key(x+dx, y+dy, z+dz) = key + (dx*H + dy)*D + dz
-  const int64_t sHD = (int64_t)H * D, sD = D;
+  const int W4 = (W + 3) >> 2, H4 = (H + 3) >> 2, D4 = (D + 3) >> 2;
   for (int p = threadIdx.x; p < nv * 27; p += 256) {
-    int li = p / 27, v = p - li * 27;
-    const int dx = v / 9 - 1, dy = v / 3 % 3 - 1, dz = v % 3 - 1;
-    int4 q = cq[li];
-    int x = q.y + dx, y = q.z + dy, z = q.w + dz;
+    const int li = p / 27, v = p - li * 27;
+    const int4 q = cq[li];
+    const int x = q.y + v / 9 - 1, y = q.z + v / 3 % 3 - 1, z = q.w + v % 3 - 1;
     uint32_t r = EMPTY;
     if (x >= 0 && x < W && y >= 0 && y < H && z >= 0 && z < D) {
-      const uint64_t k = ck[li] + (uint64_t)(dx * sHD + dy * sD + dz);
-      for (uint32_t s = home_slot(k, z, mask);; s = (s + 1) & mask) {
-        ulonglong2 e = t[s];
-        if (e.x == k) {
-          r = (uint32_t)e.y;
-          break;
-        }
-        if (e.x == HEMPTY) break;
-      }
+      const uint32_t id = brick_find(t, brick_key(q.x, x, y, z, W4, H4, D4), mask);
+      if (id != EMPTY) r = bricks[(i64)id * 64 + brick_local(x, y, z)];
     }
     nbr[v0 * 27 + p] = r;
     if (r != EMPTY) atomicOr(&gm[li], 1u << v);
@@ -191,9 +220,17 @@ SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D) {
   Tensor table = empty({(i64)cap * 2}, I64), bin = empty({n}, I32);
   ulonglong2* t = (ulonglong2*)table.p;
   k_table_clear<<<cdiv((i64)cap, 256), 256, 0, s>>>(t, (i64)cap);
-  k_table_insert<<<cdiv(n, 256), 256, 0, s>>>(coords.ptr<int4>(), n, W, H, D, t, (uint32_t)(cap - 1));
-  k_neighbors<<<cdiv(n, NV), 256, 0, s>>>(coords.ptr<int4>(), n, W, H, D, t, (uint32_t)(cap - 1),
-                                          c.nbr.ptr<uint32_t>(), c.gray.ptr<int32_t>(), bin.ptr<uint32_t>());
+  // at most n occupied bricks: the table (capacity >= 2n) never fills. Brick records are indexed by the row of
+  // the voxel that inserted the brick, so the record array has n slots (only occupied bricks' records are touched).
+  const int W4 = (W + 3) >> 2, H4 = (H + 3) >> 2, D4 = (D + 3) >> 2;
+  Tensor bricks = empty({n * 64}, I32);
+  k_brick_insert<<<cdiv(n, 256), 256, 0, s>>>(coords.ptr<int4>(), n, W4, H4, D4, t, (uint32_t)(cap - 1),
+                                              (uint4*)bricks.p);
+  k_brick_fill<<<cdiv(n, 256), 256, 0, s>>>(coords.ptr<int4>(), n, W4, H4, D4, t, (uint32_t)(cap - 1),
+                                            bricks.ptr<uint32_t>());
+  k_neighbors_brick<<<cdiv(n, NV), 256, 0, s>>>(coords.ptr<int4>(), n, W, H, D, t, (uint32_t)(cap - 1),
+                                                bricks.ptr<uint32_t>(), c.nbr.ptr<uint32_t>(),
+                                                c.gray.ptr<int32_t>(), bin.ptr<uint32_t>());
   CK(hipGetLastError());
   stable_argsort27(bin.ptr<uint32_t>(), n, c.sorted.ptr<int32_t>());
   return c;
