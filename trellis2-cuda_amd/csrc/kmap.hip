@@ -97,9 +97,11 @@ __global__ void __launch_bounds__(256) k_brick_fill(const int4* __restrict__ c, 
   bricks[(i64)id * 64 + brick_local(q.y, q.z, q.w)] = (uint32_t)i;
 }
 
-// 64 voxels x 27 offsets per workgroup, one thread per (voxel, offset) pair, so the [N,27] output is one contiguous,
-// fully coalesced range per workgroup; the 27-bit mask is assembled with LDS atomic OR and decoded
-// (gray -> binary prefix xor) by one thread per voxel.
+// 64 voxels x 27 offsets per workgroup. First each voxel's candidate bricks are looked up once: per axis its own
+// brick and, when it sits on the brick's low or high face, the brick across that face (at most 8, 3.4 on average:
+// one table probe each, not one per offset). Then one thread per (voxel, offset) pair reads the neighbour's row
+// from its brick's record, so the [N,27] output is one contiguous, fully coalesced range per workgroup; the 27-bit
+// mask is assembled with LDS atomic OR and decoded (gray -> binary prefix xor) by one thread per voxel.
 __global__ void __launch_bounds__(256) k_neighbors_brick(const int4* __restrict__ c, i64 n, int W, int H, int D,
                                                          const ulonglong2* __restrict__ t, uint32_t mask,
                                                          const uint32_t* __restrict__ bricks,
@@ -107,6 +109,7 @@ __global__ void __launch_bounds__(256) k_neighbors_brick(const int4* __restrict_
                                                          uint32_t* __restrict__ bin) {
   __shared__ int4 cq[NV];
   __shared__ uint32_t gm[NV];
+  __shared__ uint32_t bid[NV][8];  // candidate brick ids: bit 0/1/2 = the x/y/z brick across the voxel's face
   const i64 v0 = (i64)blockIdx.x * NV;
   const int nv = (int)min<i64>(NV, n - v0);
   if (threadIdx.x < NV) {
@@ -115,13 +118,28 @@ __global__ void __launch_bounds__(256) k_neighbors_brick(const int4* __restrict_
   }
   __syncthreads();
   const int W4 = (W + 3) >> 2, H4 = (H + 3) >> 2, D4 = (D + 3) >> 2;
+  // the brick across a face in one axis: -1 / +1 when the coordinate is on the brick's low / high face, else none
+  auto side = [](int x) __attribute__((always_inline)) { return (x & 3) == 0 ? -1 : ((x & 3) == 3 ? 1 : 0); };
+  for (int task = threadIdx.x; task < nv * 8; task += 256) {
+    const int li = task >> 3, cb = task & 7;
+    const int4 q = cq[li];
+    const int sx = (cb & 1) ? side(q.y) : 0, sy = (cb & 2) ? side(q.z) : 0, sz = (cb & 4) ? side(q.w) : 0;
+    const int bx = (q.y >> 2) + sx, by = (q.z >> 2) + sy, bz = (q.w >> 2) + sz;
+    uint32_t id = EMPTY;
+    const bool needed = ((cb & 1) == 0 || sx != 0) && ((cb & 2) == 0 || sy != 0) && ((cb & 4) == 0 || sz != 0);
+    if (needed && bx >= 0 && bx < W4 && by >= 0 && by < H4 && bz >= 0 && bz < D4)
+      id = brick_find(t, (((uint64_t)(uint32_t)q.x * W4 + bx) * H4 + by) * D4 + bz, mask);
+    bid[li][cb] = id;
+  }
+  __syncthreads();
   for (int p = threadIdx.x; p < nv * 27; p += 256) {
     const int li = p / 27, v = p - li * 27;
     const int4 q = cq[li];
     const int x = q.y + v / 9 - 1, y = q.z + v / 3 % 3 - 1, z = q.w + v % 3 - 1;
     uint32_t r = EMPTY;
     if (x >= 0 && x < W && y >= 0 && y < H && z >= 0 && z < D) {
-      const uint32_t id = brick_find(t, brick_key(q.x, x, y, z, W4, H4, D4), mask);
+      const int cb = ((x >> 2) != (q.y >> 2) ? 1 : 0) | ((y >> 2) != (q.z >> 2) ? 2 : 0) | ((z >> 2) != (q.w >> 2) ? 4 : 0);
+      const uint32_t id = bid[li][cb];
       if (id != EMPTY) r = bricks[(i64)id * 64 + brick_local(x, y, z)];
     }
     nbr[v0 * 27 + p] = r;
@@ -273,17 +291,32 @@ const Tensor& SpConvCache::window_order(int log2w) {
 }
 
 // tbl[i][v] = nbr[order[i]][v], gs[i] = gray[order[i]]; rows past n are EMPTY with a zero mask. One thread per
-// (row, offset) pair, so both the 108-byte source rows and the table are read and written contiguously.
-__global__ void k_row_table(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ gray,
-                            const int32_t* __restrict__ order, i64 n, i64 npad, uint32_t* __restrict__ tbl,
-                            int32_t* __restrict__ gs) {
-  const i64 p = (i64)blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= npad * 27) return;
-  const i64 i = p / 27;
-  const int v = (int)(p - i * 27);
-  const int o = i < n ? order[i] : 0;
-  tbl[p] = i < n ? nbr[(i64)o * 27 + v] : EMPTY;
-  if (v == 0) gs[i] = i < n ? gray[o] : 0;
+// row: its 108-byte source row is read as 6 x 16 + 12 bytes and written the same way, so consecutive threads write
+// one contiguous range.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+__global__ void __launch_bounds__(256) k_row_table(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ gray,
+                                                   const int32_t* __restrict__ order, i64 n, i64 npad,
+                                                   uint32_t* __restrict__ tbl, int32_t* __restrict__ gs) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= npad) return;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(nbr), 0,
+                                                                      (int)(n * 108), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(tbl, 0, (int)(npad * 108), 0x00020000);
+  const bool live = i < n;
+  const int o = live ? order[i] : 0;
+  // a padded row reads past the source end (zeros) and is then set to EMPTY
+  const uint32_t src = live ? (uint32_t)o * 108u : 0xffff0000u, dst = (uint32_t)i * 108u;
+#pragma unroll
+  for (int j = 0; j < 6; j++) {
+    u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(rs, src + j * 16, 0, 0);
+    if (!live) q = u32x4_t{EMPTY, EMPTY, EMPTY, EMPTY};
+    __builtin_amdgcn_raw_buffer_store_b128(q, rd, dst + j * 16, 0, 0);
+  }
+  u32x3_t q = __builtin_amdgcn_raw_buffer_load_b96(rs, src + 96, 0, 0);
+  if (!live) q = u32x3_t{EMPTY, EMPTY, EMPTY};
+  __builtin_amdgcn_raw_buffer_store_b96(q, rd, dst + 96, 0, 0);
+  gs[i] = live ? gray[o] : 0;
 }
 
 const SpConvCache::RowTable& SpConvCache::row_table(int log2w) {
@@ -295,7 +328,8 @@ const SpConvCache::RowTable& SpConvCache::row_table(int log2w) {
   const i64 npad = std::max<i64>(cdiv(N, kRowTablePad), 1) * kRowTablePad;
   r.tbl = empty({npad, 27}, I32);
   r.gs = empty({npad}, I32);
-  k_row_table<<<cdiv(npad * 27, 256), 256, 0, stream()>>>(nbr.ptr<uint32_t>(), gray.ptr<int32_t>(),
+  REQ(npad * 108 <= 0xfffe0000ll, "neighbour table of %lld rows too large", (long long)npad);
+  k_row_table<<<cdiv(npad, 256), 256, 0, stream()>>>(nbr.ptr<uint32_t>(), gray.ptr<int32_t>(),
                                                           r.order.ptr<int32_t>(), N, npad, r.tbl.ptr<uint32_t>(),
                                                           r.gs.ptr<int32_t>());
   CK(hipGetLastError());
