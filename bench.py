@@ -156,18 +156,44 @@ def main():
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic}
 
+    # measured ceilings on this box, for context next to the spec peaks the roofline uses: a 1 GiB device copy
+    # (read + write bytes / time) and a large dense bf16 GEMM through the vendor BLAS
+    def timed(f, reps):
+        f()
+        torch.cuda.synchronize()
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record(stream)
+        for _ in range(reps):
+            f()
+        eb.record(stream)
+        torch.cuda.synchronize()
+        return ea.elapsed_time(eb) / reps
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    copy_gbs = 2 * (1 << 30) / (timed(lambda: dst.copy_(src), 5) * 1e-3) / 1e9
+    del src, dst
+    ga = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
+    gb = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
+    gemm_tf = 2 * 8192 ** 3 / (timed(lambda: torch.mm(ga, gb), 10) * 1e-3) / 1e12
+    del ga, gb
+    measured = {"hbm_copy_GBps": round(copy_gbs, 1), "bf16_gemm_TFLOPs": round(gemm_tf, 1),
+                "frac_of_measured": round((tflops / gemm_tf) if wide else (gbs / copy_gbs), 4)}
+
     e2e = None
-    if cfg.subdivide:  # cascade upsample block end to end: subdivide -> rehash + kernel map -> conv
+    if cfg.subdivide:
+        # cascade upsample block end to end: subdivide -> rehash + kernel map -> conv of the children, which read
+        # their parents' rows through the c2s map (no gathered child features are written)
         lgt = torch.from_numpy(lg.view(np.int16)).to(dev).view(torch.float16)
+        xp = torch.randn((len(coords), ci), generator=g, device=dev).to(torch.bfloat16)
         parts = {"subdivide": [], "kmap": [], "conv": [], "total": []}
         for i in range(4):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
             ev[0].record(stream)
-            ch, _ = sp.subdivide(par, lgt)
+            ch, src = sp.subdivide(par, lgt)
             ev[1].record(stream)
             c2 = sp.build_neighbors(ch.contiguous())
             ev[2].record(stream)
-            sp.subm_conv_fused(x, w, b, c2, residual=res, act=act, out=y)
+            sp.subm_conv_gathered(xp, src, 3, w, b, c2, residual=res, act=act, out=y)
             ev[3].record(stream)
             torch.cuda.synchronize()
             if i:
@@ -219,7 +245,7 @@ def main():
         "extras": {"mvox_per_s": round(mvox, 2), "compulsory_GBps": round(gbs, 1),
                    "kmap_build_ms": round(float(np.median(map_ms)), 4), "coord_gen_s": round(gen_s, 2),
                    "executed_over_active_pairs": round(executed_pairs / max(P, 1), 4), "skip_group_rows": gsz, "wall_s": round(wall, 3),
-                   "upsample_block_e2e": e2e},
+                   "upsample_block_e2e": e2e, "measured_peaks": measured},
     }
     print(json.dumps(out), flush=True)
 

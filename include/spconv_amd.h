@@ -67,6 +67,14 @@ int spc_subm_conv(const void* x, const void* w, const void* b, int dtype, int b_
 int spc_subm_conv_fused(const void* x, const void* w, const void* b, const void* residual, int dtype, int b_dtype,
                         int res_dtype, int out_dtype, int act, int64_t N, int Ci, int Co, spc_cache* c, void* out);
 
+/* Conv of gathered rows: as spc_subm_conv_fused with x = x_src[row_map[i] >> shift] (x_src [M,Ci], row_map int32
+ * [N], N = the cache's rows; map entries outside [0,M) read zero rows), without materializing the gathered rows.
+ * With the c2s outputs (row_map = src, shift = 3) this is a decoder upsample block's gather + conv.
+ * Replaces: SDecoder's k_gather_rows followed by subm_conv (src/sdec.cu:34-43, 70-87). */
+int spc_subm_conv_gathered(const void* x_src, int64_t M, const int32_t* row_map, int shift, const void* w,
+                           const void* b, const void* residual, int dtype, int b_dtype, int res_dtype, int out_dtype,
+                           int act, int64_t N, int Ci, int Co, spc_cache* c, void* out);
+
 /* Child subdivision (c2s): children of each parent whose fp16 logit (logits [n,8]) is > 0, in (parent, slot)
  * order; child_coords int32 [>= 8n, 4] and src int32 [>= 8n] receive the children, *m (host) their count
  * (the call waits for the stream, as the reference does at src/sdec.cu:52).

@@ -178,3 +178,37 @@ def test_conv_golden_fixture(gpu):
     cache = sp.build_neighbors(torch.from_numpy(g["coords"]).to(gpu))
     y = sp.subm_conv_fused(t("x"), t("w"), t("b"), cache, residual=t("r"), act=sp.ACT_SILU, out_dtype=torch.float32)
     compare(y, g["y_silu_res"].astype(np.float32), "f32", "golden fixture")
+
+
+# ------------------------------------------------------------------------------------------ gathered rows
+@pytest.mark.parametrize("ci,co", [(128, 64), (64, 64), (32, 64), (256, 256), (64, 128)])
+def test_gathered_conv(gpu, ci, co):
+    """subm_conv_gathered on c2s children reading their parents' rows (row_map = src, shift 3) equals the conv of
+    the materialized gathered rows bit for bit, and the fp32 oracle on them; map entries outside the source rows
+    read zero rows."""
+    par = W.shell_coords(W.CONFIGS["c1"])
+    lg = W.keep_logits(len(par), 0.35, 3)
+    ch, src = sp.subdivide(torch.from_numpy(par).to(gpu),
+                           torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16))
+    print(f"gathered case parents={len(par)} children={len(ch)} ci={ci} co={co}", flush=True)
+    cache = sp.build_neighbors(ch.contiguous())
+    cfg = W.Config("t", 0, 0, (0, 0), False, 0, ci, co, "bf16", "", 77)
+    w, b = W.conv_params(cfg)
+    tx, qx = quantize(W.features(len(par), ci, 5), "bf16")
+    tw, qw = quantize(w, "bf16")
+    tr, qr = quantize(W.features(len(ch), co, 6), "bf16")
+    xs, ws, bs, rs = tx.to(gpu), tw.to(gpu), torch.from_numpy(b).to(gpu), tr.to(gpu)
+    rmap = src.clone()
+    rmap[::97] = (len(par) + 3) * 8  # past the source rows
+    rmap[5::101] = -8                # negative
+    for act in (0, 1):
+        y1 = sp.subm_conv_gathered(xs, rmap, 3, ws, bs, cache, residual=rs, act=act, out_dtype=torch.float32)
+        idx = rmap.long() >> 3
+        ok = (idx >= 0) & (idx < len(par))
+        xg = torch.zeros((len(ch), ci), dtype=torch.bfloat16, device=gpu)
+        xg[ok] = xs[idx[ok]]
+        y2 = sp.subm_conv_fused(xg, ws, bs, cache, residual=rs, act=act, out_dtype=torch.float32)
+        assert torch.equal(y1, y2), f"ci={ci} co={co} act={act}: gathered != materialized"
+        nbr, _, _, _ = oracle.build_neighbors(ch.cpu().numpy())
+        ref = oracle.conv(xg.float().cpu().numpy(), qw, b, nbr, res=qr, act=act)
+        compare(y1, ref, "f32", f"gathered ci={ci} co={co} act={act}")

@@ -106,6 +106,25 @@ SPC_API int spc_subm_conv_fused(const void* x, const void* w, const void* b, con
   });
 }
 
+SPC_API int spc_subm_conv_gathered(const void* x_src, int64_t M, const int32_t* row_map, int shift, const void* w,
+                                   const void* b, const void* residual, int dtype, int b_dtype, int res_dtype,
+                                   int out_dtype, int act, int64_t N, int Ci, int Co, spc_cache* c, void* out) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    REQ(N == c->c.N, "N=%lld but the cache has %d rows", (long long)N, c->c.N);
+    REQ(M >= 0 && Ci > 0 && Co > 0, "M=%lld Ci=%d Co=%d", (long long)M, Ci, Co);
+    REQ(N == 0 || (x_src && row_map && w && out && M > 0), "null x_src/row_map/w/out or M = 0");
+    DT dt = float_dt(dtype, "x/w");
+    REQ(dt != F32, "x/w must be fp16 or bf16");
+    Tensor tx = borrow(x_src, {M, Ci}, dt), tw = borrow(w, {Co, 27, Ci}, dt), tm = borrow(row_map, {N}, I32);
+    Tensor tb, tr, to = borrow(out, {N, Co}, float_dt(out_dtype, "out"));
+    if (b) tb = borrow(b, {Co}, float_dt(b_dtype, "bias"));
+    if (residual) tr = borrow(residual, {N, Co}, float_dt(res_dtype, "residual"));
+    if (N == 0) return;
+    subm_conv_gathered(tx, tm, shift, tw, b ? &tb : nullptr, residual ? &tr : nullptr, act, c->c, to);
+  });
+}
+
 SPC_API int spc_subm_conv(const void* x, const void* w, const void* b, int dtype, int b_dtype, int64_t N, int Ci,
                           int Co, spc_cache* c, void* out) {
   return spc_subm_conv_fused(x, w, b, nullptr, dtype, b_dtype, SPC_F32, dtype, SPC_ACT_NONE, N, Ci, Co, c, out);

@@ -1134,10 +1134,27 @@ SpConvCfg spconv_cfg(int N, int Ci, int Co) {
   return SpConvCfg{128, Ci % 64 == 0 ? 64 : 32, 1};
 }
 
-void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Tensor* residual, int act,
-                     SpConvCache& c, Tensor& out) {
+// The kernels that read their tiles' neighbour rows from the tile-order table (narrow, 256-channel wide) can read
+// them through a row map instead; the others get the gathered rows materialized.
+bool reads_row_table(const SpConvCfg& cfg, int Ci, int Co) {
+  return (Co == 64 && Ci <= 128) || (cfg.BK == 64 && Co % 256 == 0);
+}
+
+__global__ void k_gather_rows(const u32x4* __restrict__ x, i64 m, int units, const int32_t* __restrict__ row_map,
+                              int shift, i64 n, u32x4* __restrict__ out) {
+  const i64 q = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= n * units) return;
+  const i64 i = q / units;
+  const uint32_t r = (uint32_t)row_map[i] >> shift;
+  out[q] = r < (uint64_t)m ? x[(i64)r * units + (q - i * units)] : u32x4{0, 0, 0, 0};
+}
+
+// x: the conv input [N,Ci], or with row_map the source rows [M,Ci] read through row_map >> shift
+void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& w, const Tensor* b,
+               const Tensor* residual, int act, SpConvCache& c, Tensor& out) {
   REQ(x.dim() == 2 && w.dim() == 3, "x must be [N,Ci], w [Co,27,Ci]");
-  const int N = (int)x.size(0), Ci = (int)x.size(1), Co = (int)w.size(0);
+  const int N = row_map ? c.N : (int)x.size(0), Ci = (int)x.size(1), Co = (int)w.size(0);
+  const i64 M = x.size(0);
   REQ((x.dt == BF16 || x.dt == F16) && w.dt == x.dt, "x and w must both be bf16 or both fp16 (x %s, w %s)",
       dname(x.dt), dname(w.dt));
   REQ(w.size(1) == 27 && w.size(2) == Ci, "w must be [Co,27,%d]", Ci);
@@ -1176,9 +1193,9 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   a.order = c.sorted.ptr<int32_t>();
   a.gray = c.gray.ptr<int32_t>();
   a.code = code.ptr<uint32_t>();
-  REQ((uint64_t)N * Ci * 2 <= kMaxBufferBytes && (uint64_t)Co * 27 * Ci * 2 <= kMaxBufferBytes,
+  REQ((uint64_t)M * Ci * 2 <= kMaxBufferBytes && (uint64_t)Co * 27 * Ci * 2 <= kMaxBufferBytes,
       "x or w larger than %llu bytes", (unsigned long long)kMaxBufferBytes);
-  a.x_bytes = (uint32_t)((uint64_t)N * Ci * 2);
+  a.x_bytes = (uint32_t)((uint64_t)M * Ci * 2);
   REQ(((uint64_t)N + SpConvCache::kRowTablePad) * 108 <= kMaxBufferBytes, "neighbour table larger than %llu bytes",
       (unsigned long long)kMaxBufferBytes);
   a.nbr_bytes = (uint32_t)((uint64_t)N * 108);
@@ -1195,15 +1212,17 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   a.Ci = Ci;
   a.Co = Co;
   a.act = act;
-  Tensor wpack;
+  Tensor wpack, mtbl;
+  REQ(!row_map || reads_row_table(cfg, Ci, Co), "row map with a kernel that reads nbr directly");
   const i64 chunks = (i64)Co * 27 * Ci / 8;
   if (Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, rows in spatial order
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
     const SpConvCache::RowTable& rt = c.row_table(16);
+    if (row_map) mtbl = c.mapped_table(16, *row_map, shift, M);
     a.order = rt.order.ptr<int32_t>();
-    a.tbl = rt.tbl.ptr<uint32_t>();
+    a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
     a.gs = rt.gs.ptr<int32_t>();
     a.tbl_bytes = (uint32_t)rt.tbl.bytes();
   } else if (cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
@@ -1212,7 +1231,8 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
     a.w = wpack.ptr<uint16_t>();
     if (Co % 256 == 0) {  // the 256 x 256 kernel reads its tiles' neighbour rows from the sorted-order table
       const SpConvCache::RowTable& rt = c.row_table(-1);
-      a.tbl = rt.tbl.ptr<uint32_t>();
+      if (row_map) mtbl = c.mapped_table(-1, *row_map, shift, M);
+      a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
       a.gs = rt.gs.ptr<int32_t>();
       a.tbl_bytes = (uint32_t)rt.tbl.bytes();
     }
@@ -1220,6 +1240,30 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
   if (x.dt == F16) dispatch<true>(cfg, a);
   else dispatch<false>(cfg, a);
   CK(hipGetLastError());
+}
+
+void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Tensor* residual, int act,
+                     SpConvCache& c, Tensor& out) {
+  conv_impl(x, nullptr, 0, w, b, residual, act, c, out);
+}
+
+void subm_conv_gathered(const Tensor& x_src, const Tensor& row_map, int shift, const Tensor& w, const Tensor* b,
+                        const Tensor* residual, int act, SpConvCache& c, Tensor& out) {
+  REQ(x_src.dim() == 2 && w.dim() == 3, "x_src must be [M,Ci], w [Co,27,Ci]");
+  REQ(row_map.dt == I32 && row_map.numel() == c.N, "row_map must be int32 [%d]", c.N);
+  REQ(shift >= 0 && shift < 31, "shift=%d", shift);
+  const int Ci = (int)x_src.size(1), Co = (int)w.size(0);
+  REQ(Ci > 0 && Ci % 32 == 0 && Ci <= kMaxCi, "Ci=%d must be a multiple of 32 (at most %d)", Ci, kMaxCi);
+  if (c.N == 0 || reads_row_table(spconv_cfg(c.N, Ci, Co), Ci, Co)) {
+    conv_impl(x_src, &row_map, shift, w, b, residual, act, c, out);
+    return;
+  }
+  Tensor xg = empty({(i64)c.N, Ci}, x_src.dt);
+  const int units = Ci * 2 / 16;
+  k_gather_rows<<<cdiv((i64)c.N * units, 256), 256, 0, stream()>>>((const u32x4*)x_src.p, x_src.size(0), units,
+                                                                   row_map.ptr<int32_t>(), shift, c.N, (u32x4*)xg.p);
+  CK(hipGetLastError());
+  conv_impl(xg, nullptr, 0, w, b, residual, act, c, out);
 }
 
 Tensor subm_conv(const Tensor& x, const Tensor& w, const Tensor* b, SpConvCache& c) {

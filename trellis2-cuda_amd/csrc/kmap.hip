@@ -336,6 +336,28 @@ const SpConvCache::RowTable& SpConvCache::row_table(int log2w) {
   return rtab.emplace(key, r).first->second;
 }
 
+// mapped rows outside [0, m) become EMPTY, so the conv reads zeros for them
+__global__ void k_map_table(const uint32_t* __restrict__ tbl, i64 entries, const int32_t* __restrict__ row_map,
+                            int shift, uint32_t m, uint32_t* __restrict__ out) {
+  const i64 e = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= entries) return;
+  const uint32_t r = tbl[e];
+  const uint32_t q = r == EMPTY ? EMPTY : (uint32_t)row_map[r] >> shift;
+  out[e] = q < m ? q : EMPTY;
+}
+
+Tensor SpConvCache::mapped_table(int log2w, const Tensor& row_map, int shift, i64 m) {
+  REQ(row_map.dt == I32 && row_map.numel() == N, "row_map must be int32 [%d]", N);
+  REQ(shift >= 0 && shift < 31, "shift=%d", shift);
+  const RowTable& rt = row_table(log2w);
+  Tensor t = empty(rt.tbl.sh, I32);
+  const i64 entries = rt.tbl.numel();
+  k_map_table<<<cdiv(entries, 256), 256, 0, stream()>>>(rt.tbl.ptr<uint32_t>(), entries, row_map.ptr<int32_t>(), shift,
+                                                        (uint32_t)std::min<i64>(m, EMPTY), t.ptr<uint32_t>());
+  CK(hipGetLastError());
+  return t;
+}
+
 const std::pair<Tensor, Tensor>& SpConvCache::valid(int B1) {
   auto it = vk.find(B1);
   if (it != vk.end()) return it->second;

@@ -36,6 +36,9 @@ struct SpConvCache {
   };
   std::map<int, RowTable> rtab;
   const RowTable& row_table(int log2w);
+  // row_table(log2w).tbl with every non-EMPTY entry r replaced by row_map[r] >> shift, or EMPTY when that is not
+  // below m (not memoized: row_map is the caller's). Used by the gathered conv.
+  Tensor mapped_table(int log2w, const Tensor& row_map, int shift, i64 m);
 };
 SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D);  // coords int32 [N,4] (b,x,y,z)
 
@@ -55,6 +58,13 @@ enum SpAct : int { ACT_NONE = 0, ACT_SILU = 1 };
 // residual may be null; out must be a defined [N,Co] tensor of dtype F32, F16 or BF16.
 void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Tensor* residual, int act,
                      SpConvCache& c, Tensor& out);
+
+// Conv of gathered rows without materializing them: out = subm_conv_fused(x_src[row_map >> shift], ...).
+// x_src [M,Ci]; row_map int32 [N] (N = the cache's rows), e.g. the c2s parent map (src, shift 3), so a decoder's
+// upsample block (reference src/sdec.cu:34-43 k_gather_rows then the conv at :70-87) reads the parent rows
+// directly. Entries outside [0, M) read as zero rows.
+void subm_conv_gathered(const Tensor& x_src, const Tensor& row_map, int shift, const Tensor& w, const Tensor* b,
+                        const Tensor* residual, int act, SpConvCache& c, Tensor& out);
 
 // Child subdivision of a sparse level (reference src/sdec.cu:20-57): children of each parent whose fp16 logit is
 // > 0, in (parent, slot) order, coords (b, 2x+(s&1), 2y+(s>>1&1), 2z+(s>>2&1)), src = parent*8+s.

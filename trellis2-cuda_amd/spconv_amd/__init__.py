@@ -25,7 +25,8 @@ EMPTY = 0xFFFFFFFF
 
 # the C ABI's exported symbols (every declaration of include/spconv_amd.h)
 SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_cache_free", "spc_cache_info",
-           "spc_cache_valid", "spc_conv_cfg", "spc_subm_conv", "spc_subm_conv_fused", "spc_subdivide")
+           "spc_cache_valid", "spc_conv_cfg", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
+           "spc_subdivide")
 
 _lib = None
 
@@ -50,6 +51,7 @@ def load_library():
     L.spc_conv_cfg.argtypes = [I64, I, I, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)]
     L.spc_subm_conv.argtypes = [P, P, P, I, I, I64, I, I, P, P]
     L.spc_subm_conv_fused.argtypes = [P, P, P, P, I, I, I, I, I, I64, I, I, P, P]
+    L.spc_subm_conv_gathered.argtypes = [P, I64, P, I, P, P, P, I, I, I, I, I, I64, I, I, P, P]
     L.spc_subdivide.argtypes = [P, P, I64, P, P, ctypes.POINTER(I64)]
     for name in SYMBOLS:
         if name != "spc_last_error":
@@ -181,6 +183,27 @@ def subm_conv_fused(x, w, b, cache: SpConvCache, residual=None, act: int = ACT_N
     _check(load_library().spc_subm_conv_fused(
         _ptr(x), _ptr(w), _ptr(b), _ptr(residual), _dt(x), _dt(b) if b is not None else F32,
         _dt(residual) if residual is not None else F32, _dt(out), act, N, Ci, Co, cache._h, _ptr(out)))
+    return out
+
+
+def subm_conv_gathered(x_src, row_map, shift: int, w, b, cache: SpConvCache, residual=None, act: int = ACT_NONE,
+                       out=None, out_dtype=None):
+    """subm_conv_fused on x = x_src[row_map >> shift] without materializing it (e.g. c2s children reading their
+    parents' rows: row_map = src, shift = 3). Map entries outside [0, len(x_src)) read zero rows."""
+    torch = _torch()
+    M, Ci = x_src.shape
+    N = cache.N
+    Co = w.shape[0]
+    if w.dtype != x_src.dtype:
+        raise ValueError(f"x_src and w must both be bf16 or both fp16 (x {x_src.dtype}, w {w.dtype})")
+    if row_map.dtype != torch.int32 or row_map.numel() != N:
+        raise ValueError(f"row_map must be int32 [{N}]")
+    if out is None:
+        out = torch.empty((N, Co), dtype=out_dtype or x_src.dtype, device=x_src.device)
+    _check(load_library().spc_subm_conv_gathered(
+        _ptr(x_src), M, _ptr(row_map), shift, _ptr(w), _ptr(b), _ptr(residual), _dt(x_src),
+        _dt(b) if b is not None else F32, _dt(residual) if residual is not None else F32, _dt(out), act, N, Ci, Co,
+        cache._h, _ptr(out)))
     return out
 
 
