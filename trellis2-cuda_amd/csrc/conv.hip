@@ -874,10 +874,12 @@ void launch_narrow(ConvArgs a) {
 //  * Ring protocol per stage s: wait (counted vmcnt) for this lane's DMA of A(s), barrier (every wavefront's
 //    part has landed and everyone is done with stage s-1), then, between the MFMA groups of stage s, refill the
 //    slot stage s-1 used with A(s+3) and load the weights of stage s+1 into the other register set.
-template <bool F16>
-__global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
-  constexpr int NW = 4, NT = 256, BM = 256, KC = 64, PC = KC / 8;
-  constexpr int TM = 8, TN = 2, AL = BM * PC / NT;  // AL = 8 DMA loads per lane per stage
+template <bool F16, int BM>
+__global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvArgs a) {
+  constexpr int NW = 4, NT = 256, KC = 64, PC = KC / 8;
+  constexpr int TM = BM / 32, TN = 2, AL = BM * PC / NT;  // AL = TM DMA loads per lane per stage
+  constexpr int BQ = 8 / TM;                            // weight loads per 32-row group (8 per stage)
+  static_assert(BM == 128 || BM == 256, "tile rows");
   __shared__ __attribute__((aligned(16))) u32x4 As0[BM * PC], As1[BM * PC], As2[BM * PC], As3[BM * PC];
   __shared__ uint32_t srcT[BM * 27];
   __shared__ int ordT[BM];
@@ -895,7 +897,7 @@ __global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
 
   // prologue: the tile's block of the neighbour table goes to LDS by DMA; rows and 32-row masks from the same order
   dma_tile_table<BM, NT>(a, row0, srcT, tid);
-  {
+  if (tid < BM) {
     const int row = row0 + tid;
     ordT[tid] = row < N ? a.order[row] : 0;
     uint32_t gm = a.gs[row];  // padded rows have mask 0
@@ -980,7 +982,9 @@ __global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       dma(fill, i, off[i], ka);
-      rbN[i / 4][i % 4] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + i * 1024, soff, 0);
+#pragma unroll
+      for (int q = i * BQ; q < (i + 1) * BQ; q++)
+        rbN[q / 4][q % 4] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + q * 1024, soff, 0);
       if (i + 1 < TM) read_fa(fa[(i + 1) & 1], i + 1);
       if (gms[i] & vbit) {
 #pragma unroll
@@ -991,12 +995,13 @@ __global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
     }
   };
   // loads issued after this lane's last DMA of A(s) when stage s starts: prologue DMAs and B(0) for s < 3,
-  // then (in steady state) one weight load of stage s-3 plus two full stages of 16
+  // then (in steady state) the last group's weight loads of stage s-3 plus two full stages of AL + 8
+  constexpr int SL = AL + 8;
   auto wait_a = [&](int s) __attribute__((always_inline)) {
     if (s == 0) wait_vmcnt<2 * AL + 8>();
-    else if (s == 1) wait_vmcnt<AL + 8 + 16>();
-    else if (s == 2) wait_vmcnt<8 + 2 * 16>();
-    else wait_vmcnt<1 + 2 * 16>();
+    else if (s == 1) wait_vmcnt<AL + 8 + SL>();
+    else if (s == 2) wait_vmcnt<8 + 2 * SL>();
+    else wait_vmcnt<BQ + 2 * SL>();
   };
 
   if (total > 0) {
@@ -1038,9 +1043,9 @@ __global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
   wait_vmcnt<0>();
   __syncthreads();
 
-  // epilogue through this wavefront's share of the (now idle) ring
-  float* ew = (wn < 2 ? (float*)&As0[0] : (float*)&As1[0]) + (wn & 1) * (32 * 72);
-  static_assert(2 * 32 * 72 * 4 <= BM * PC * 16, "two wavefronts' epilogue staging fits in one ring slot");
+  // epilogue through the (now idle) ring: one slot per wavefront
+  float* ew = (float*)(wn == 0 ? &As0[0] : wn == 1 ? &As1[0] : wn == 2 ? &As2[0] : &As3[0]);
+  static_assert(32 * 72 * 4 <= BM * PC * 16, "a wavefront's epilogue staging fits in one ring slot");
   const int co_w = co0 + wn * 64;
   float bias8[8];
 #pragma unroll
@@ -1050,13 +1055,31 @@ __global__ void __launch_bounds__(256) k_conv_wide_dma(ConvArgs a) {
   epilogue_tile<TM, TN>(acc, ew, ordT, nrows, co_w, bias8, e, a.Co, lane);
 }
 
-template <bool F16>
-void launch_wide_dma(ConvArgs a) {
-  a.tiles_m = cdiv(a.N, 256);
+int cu_count() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    CK(hipGetDevice(&dev));
+    CK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  return n;
+}
+
+// 256-row tiles (one workgroup per CU) unless that leaves fewer than two tiles per CU: then 128-row tiles, two
+// workgroups per CU, so a small-N wide layer (C2: 297 tiles of 256 rows for 256 CUs) does not spend its second
+// round on a few tiles.
+template <bool F16, int BM>
+void launch_wide_dma_bm(ConvArgs a) {
+  a.tiles_m = cdiv(a.N, BM);
   a.tiles_n = a.Co / 256;
   int tiles = a.tiles_m * a.tiles_n;
   a.grid = (tiles + 7) / 8 * 8;
-  k_conv_wide_dma<F16><<<a.grid, 256, 0, stream()>>>(a);
+  k_conv_wide_dma<F16, BM><<<a.grid, 256, 0, stream()>>>(a);
+}
+template <bool F16>
+void launch_wide_dma(ConvArgs a) {
+  if ((i64)cdiv(a.N, 256) * (a.Co / 256) < 2 * (i64)cu_count()) launch_wide_dma_bm<F16, 128>(a);
+  else launch_wide_dma_bm<F16, 256>(a);
 }
 
 template <bool F16, int NW, int BM>
