@@ -45,6 +45,7 @@ def main():
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured copy / GEMM ceilings")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy (the counter calibration used by bench_profile.py)")
     args = ap.parse_args()
@@ -168,16 +169,18 @@ def main():
         eb.record(stream)
         torch.cuda.synchronize()
         return ea.elapsed_time(eb) / reps
-    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    dst = torch.empty_like(src)
-    copy_gbs = 2 * (1 << 30) / (timed(lambda: dst.copy_(src), 5) * 1e-3) / 1e9
-    del src, dst
-    ga = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
-    gb = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
-    gemm_tf = 2 * 8192 ** 3 / (timed(lambda: torch.mm(ga, gb), 10) * 1e-3) / 1e12
-    del ga, gb
-    measured = {"hbm_copy_GBps": round(copy_gbs, 1), "bf16_gemm_TFLOPs": round(gemm_tf, 1),
-                "frac_of_measured": round((tflops / gemm_tf) if wide else (gbs / copy_gbs), 4)}
+    measured = None
+    if not args.no_peaks:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        copy_gbs = 2 * (1 << 30) / (timed(lambda: dst.copy_(src), 5) * 1e-3) / 1e9
+        del src, dst
+        ga = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
+        gb = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
+        gemm_tf = 2 * 8192 ** 3 / (timed(lambda: torch.mm(ga, gb), 10) * 1e-3) / 1e12
+        del ga, gb
+        measured = {"hbm_copy_GBps": round(copy_gbs, 1), "bf16_gemm_TFLOPs": round(gemm_tf, 1),
+                    "frac_of_measured": round((tflops / gemm_tf) if wide else (gbs / copy_gbs), 4)}
 
     e2e = None
     if cfg.subdivide:
