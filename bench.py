@@ -205,6 +205,32 @@ def main():
                 parts["conv"].append(ev[2].elapsed_time(ev[3]))
                 parts["total"].append(ev[0].elapsed_time(ev[3]))
         e2e = {k + "_ms": round(float(np.median(v)), 4) for k, v in parts.items()}
+        # the reference block's second half on the same children (src/sdec.cu:76-84): conv1's output h1 [n, 8*Co]
+        # (random here) -> child rows -> LayerNorm -> SiLU -> conv2 (Co -> Co) -> skip add from the parents' x
+        co2 = co
+        h1 = torch.randn((len(coords) * 8, co2), generator=g, device=dev).to(torch.bfloat16)
+        w2 = (torch.randn((co2, 27, co2), generator=g, device=dev) * 0.05).to(torch.bfloat16)
+        b2 = torch.zeros(co2, device=dev)
+        y2 = torch.empty((len(ch), co2), dtype=torch.bfloat16, device=dev)
+
+        def half_gathered_rows():
+            sp.subm_conv_fused(sp.gather_ln_act(h1, src, 0), w2, b2, c2, out=y2)
+            sp.add_skip(y2, xp, src)
+
+        def half_gathered_conv():
+            sp.subm_conv_gathered(sp.gather_ln_act(h1), src, 0, w2, b2, c2, out=y2)
+            sp.add_skip(y2, xp, src)
+
+        def torch_preact():
+            torch.nn.functional.silu(torch.nn.functional.layer_norm(h1[src.long()].float(), (co2,), eps=1e-6)).to(
+                torch.bfloat16)
+        e2e["second_half"] = {
+            "children": len(ch), "Co": co2,
+            "gather_ln_silu_then_conv_ms": round(timed(half_gathered_rows, 10), 4),
+            "ln_silu_parents_then_gathered_conv_ms": round(timed(half_gathered_conv, 10), 4),
+            "gather_ln_silu_ms": round(timed(lambda: sp.gather_ln_act(h1, src, 0), 20), 4),
+            "torch_gather_ln_silu_ms": round(timed(torch_preact, 20), 4),
+            "add_skip_ms": round(timed(lambda: sp.add_skip(y2, xp, src), 20), 4)}
 
     cpu = None
     if not args.no_cpu:

@@ -75,6 +75,22 @@ int spc_subm_conv_gathered(const void* x_src, int64_t M, const int32_t* row_map,
                            const void* b, const void* residual, int dtype, int b_dtype, int res_dtype, int out_dtype,
                            int act, int64_t N, int Ci, int Co, spc_cache* c, void* out);
 
+/* Pre-activation in one pass: out[i] = act(LayerNorm(x_src[row_map[i] >> shift]) * gamma + beta), statistics in
+ * fp32, one rounding; x_src [M,C] and out [N,C] both `dtype` (SPC_F16/SPC_BF16), gamma/beta f32 [C] or NULL,
+ * act SPC_ACT_NONE/SPC_ACT_SILU, C = 8 * 2^k <= 4096. Map entries outside [0,M) read zero rows (out = act(beta));
+ * row_map NULL is the identity (N = M).
+ * Replaces: layer_norm + act_(SILU) (src/ops.cu:30-75, src/sdec.cu:72-73) and, with row_map = the c2s src and
+ * shift = 3, k_gather_rows + layer_norm + act_ (src/sdec.cu:34-43, 78-83). */
+int spc_gather_ln_act(const void* x_src, int64_t M, int C, const int32_t* row_map, int shift, const float* gamma,
+                      const float* beta, float eps, int act, int dtype, int64_t N, void* out);
+
+/* Skip connection of the upsample block, in place: h[i,c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep] with
+ * rep = Co / (Cin/8), the fp32 sum rounded once to `dtype` (bit-identical to the reference); h [m,Co], x [n,Cin],
+ * both SPC_F16 or SPC_BF16, 16-byte aligned; Cin % 8 == 0, Co % 8 == 0, Co % (Cin/8) == 0. src entries outside
+ * [0, 8n) leave their row unchanged.
+ * Replaces: k_add_skip (src/sdec.cu:38-43, launched at :84). */
+int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, int Co, int64_t n, int Cin, int dtype);
+
 /* Child subdivision (c2s): children of each parent whose fp16 logit (logits [n,8]) is > 0, in (parent, slot)
  * order; child_coords int32 [>= 8n, 4] and src int32 [>= 8n] receive the children, *m (host) their count
  * (the call waits for the stream, as the reference does at src/sdec.cu:52).

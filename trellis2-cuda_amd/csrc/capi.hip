@@ -125,6 +125,37 @@ SPC_API int spc_subm_conv_gathered(const void* x_src, int64_t M, const int32_t* 
   });
 }
 
+SPC_API int spc_gather_ln_act(const void* x_src, int64_t M, int C, const int32_t* row_map, int shift,
+                              const float* gamma, const float* beta, float eps, int act, int dtype, int64_t N,
+                              void* out) {
+  return guarded([&] {
+    REQ(M >= 0 && N >= 0 && C > 0, "M=%lld N=%lld C=%d", (long long)M, (long long)N, C);
+    DT dt = float_dt(dtype, "x");
+    REQ(dt != F32, "x must be fp16 or bf16");
+    if (N == 0) return;
+    REQ(row_map || N == M, "without a row map N (%lld) must equal M (%lld)", (long long)N, (long long)M);
+    REQ(x_src && out && M > 0, "null x_src/out or M = 0");
+    Tensor tx = borrow(x_src, {M, C}, dt), to = borrow(out, {N, C}, dt), tm, tg, tb;
+    if (row_map) tm = borrow(row_map, {N}, I32);
+    if (gamma) tg = borrow(gamma, {C}, F32);
+    if (beta) tb = borrow(beta, {C}, F32);
+    gather_ln_act(tx, row_map ? &tm : nullptr, shift, gamma ? &tg : nullptr, beta ? &tb : nullptr, eps, act, to);
+  });
+}
+
+SPC_API int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, int Co, int64_t n, int Cin,
+                         int dtype) {
+  return guarded([&] {
+    REQ(m >= 0 && n >= 0 && Co > 0 && Cin > 0, "m=%lld n=%lld Co=%d Cin=%d", (long long)m, (long long)n, Co, Cin);
+    DT dt = float_dt(dtype, "h/x");
+    REQ(dt != F32, "h/x must be fp16 or bf16");
+    if (m == 0) return;
+    REQ(h && x && src, "null h/x/src");
+    Tensor th = borrow(h, {m, Co}, dt);
+    add_skip(th, borrow(x, {n, Cin}, dt), borrow(src, {m}, I32));
+  });
+}
+
 SPC_API int spc_subm_conv(const void* x, const void* w, const void* b, int dtype, int b_dtype, int64_t N, int Ci,
                           int Co, spc_cache* c, void* out) {
   return spc_subm_conv_fused(x, w, b, nullptr, dtype, b_dtype, SPC_F32, dtype, SPC_ACT_NONE, N, Ci, Co, c, out);

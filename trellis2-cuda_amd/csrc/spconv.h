@@ -66,6 +66,18 @@ void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Te
 void subm_conv_gathered(const Tensor& x_src, const Tensor& row_map, int shift, const Tensor& w, const Tensor* b,
                         const Tensor* residual, int act, SpConvCache& c, Tensor& out);
 
+// Pre-activation of an upsample block's convs in one pass (reference src/sdec.cu:72-73, 78-83): out[i] =
+// act(LayerNorm(x_src[row_map[i] >> shift]) * gamma + beta) with fp32 statistics and one rounding; x_src bf16/fp16
+// [M,C], out [N,C] of the same dtype, gamma/beta f32 [C] or null, act ACT_NONE / ACT_SILU. Map entries outside
+// [0,M) read zero rows; a null row_map is the identity (N = M).
+void gather_ln_act(const Tensor& x_src, const Tensor* row_map, int shift, const Tensor* gamma, const Tensor* beta,
+                   float eps, int act, Tensor& out);
+
+// Skip connection of the upsample block, in place (reference k_add_skip, src/sdec.cu:38-43):
+// h[i, c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep], rep = Co / (Cin/8), fp32 sum rounded once (bit-identical
+// to the reference). h [m,Co] and x [n,Cin] of one dtype (fp16/bf16); entries of src outside x leave the row.
+void add_skip(Tensor& h, const Tensor& x, const Tensor& src);
+
 // Child subdivision of a sparse level (reference src/sdec.cu:20-57): children of each parent whose fp16 logit is
 // > 0, in (parent, slot) order, coords (b, 2x+(s&1), 2y+(s>>1&1), 2z+(s>>2&1)), src = parent*8+s.
 struct Subdivision {

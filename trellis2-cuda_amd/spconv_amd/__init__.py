@@ -26,7 +26,7 @@ EMPTY = 0xFFFFFFFF
 # the C ABI's exported symbols (every declaration of include/spconv_amd.h)
 SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_cache_free", "spc_cache_info",
            "spc_cache_valid", "spc_conv_cfg", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
-           "spc_subdivide")
+           "spc_gather_ln_act", "spc_add_skip", "spc_subdivide")
 
 _lib = None
 
@@ -52,6 +52,8 @@ def load_library():
     L.spc_subm_conv.argtypes = [P, P, P, I, I, I64, I, I, P, P]
     L.spc_subm_conv_fused.argtypes = [P, P, P, P, I, I, I, I, I, I64, I, I, P, P]
     L.spc_subm_conv_gathered.argtypes = [P, I64, P, I, P, P, P, I, I, I, I, I, I64, I, I, P, P]
+    L.spc_gather_ln_act.argtypes = [P, I64, I, P, I, P, P, ctypes.c_float, I, I, I64, P]
+    L.spc_add_skip.argtypes = [P, P, P, I64, I, I64, I, I]
     L.spc_subdivide.argtypes = [P, P, I64, P, P, ctypes.POINTER(I64)]
     for name in SYMBOLS:
         if name != "spc_last_error":
@@ -205,6 +207,41 @@ def subm_conv_gathered(x_src, row_map, shift: int, w, b, cache: SpConvCache, res
         _dt(b) if b is not None else F32, _dt(residual) if residual is not None else F32, _dt(out), act, N, Ci, Co,
         cache._h, _ptr(out)))
     return out
+
+
+def gather_ln_act(x_src, row_map=None, shift: int = 0, gamma=None, beta=None, eps: float = 1e-6,
+                  act: int = ACT_SILU, out=None):
+    """act(LayerNorm(x_src[row_map >> shift]) * gamma + beta) in one pass, fp32 statistics, one rounding to
+    x_src's dtype (reference layer_norm + act_ SILU, src/ops.cu:30-75, and the upsample block's gather before them,
+    src/sdec.cu:78-83). row_map None: the rows of x_src in order. Map entries outside [0, len(x_src)) read zero
+    rows."""
+    torch = _torch()
+    M, C = x_src.shape
+    if row_map is not None and (row_map.dtype != torch.int32 or row_map.dim() != 1):
+        raise ValueError("row_map must be int32 [N]")
+    N = M if row_map is None else row_map.numel()
+    for name, t in (("gamma", gamma), ("beta", beta)):
+        if t is not None and (t.dtype != torch.float32 or t.numel() != C):
+            raise ValueError(f"{name} must be float32 [{C}]")
+    if out is None:
+        out = torch.empty((N, C), dtype=x_src.dtype, device=x_src.device)
+    _check(load_library().spc_gather_ln_act(_ptr(x_src), M, C, _ptr(row_map), shift, _ptr(gamma), _ptr(beta),
+                                            eps, act, _dt(x_src), N, _ptr(out)))
+    return out
+
+
+def add_skip(h, x, src):
+    """In place: h += repeat_interleave(C2S(x), Co / (Cin/8), dim=1), i.e. child row i, channel c gets
+    x[src[i] >> 3, (src[i] & 7) * Cin/8 + c // rep] (reference k_add_skip, src/sdec.cu:38-43); returns h."""
+    torch = _torch()
+    m, Co = h.shape
+    n, Cin = x.shape
+    if h.dtype != x.dtype:
+        raise ValueError(f"h and x must share a dtype ({h.dtype}, {x.dtype})")
+    if src.dtype != torch.int32 or src.numel() != m:
+        raise ValueError(f"src must be int32 [{m}]")
+    _check(load_library().spc_add_skip(_ptr(h), _ptr(x), _ptr(src), m, Co, n, Cin, _dt(h)))
+    return h
 
 
 def subm_conv(x, w, b, cache: SpConvCache):
