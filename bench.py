@@ -232,6 +232,29 @@ def main():
             "torch_gather_ln_silu_ms": round(timed(torch_preact, 20), 4),
             "add_skip_ms": round(timed(lambda: sp.add_skip(y2, xp, src), 20), 4)}
 
+    # the decoder's ConvNeXt tail on this layer's output rows (LayerNorm + affine -> Linear 4C + SiLU -> Linear C ->
+    # + x, reference src/sdec.cu:60-66), fused, against torch's unfused sequence on the same tensors
+    tail = None
+    if co in (64, 128, 256):
+        hx = torch.randn((n, co), generator=g, device=dev).to(torch.bfloat16)
+        xx = torch.randn((n, co), generator=g, device=dev).to(torch.bfloat16)
+        gm, bt = torch.ones(co, device=dev), torch.zeros(co, device=dev)
+        w1 = (torch.randn((4 * co, co), generator=g, device=dev) / co ** 0.5).to(torch.bfloat16)
+        w2 = (torch.randn((co, 4 * co), generator=g, device=dev) / (2 * co)).to(torch.bfloat16)
+        b1, b2 = torch.zeros(4 * co, device=dev), torch.zeros(co, device=dev)
+        yt = torch.empty_like(hx)
+        t_f = timed(lambda: sp.convnext_mlp(hx, xx, gm, bt, w1, b1, w2, b2, out=yt), 10)
+
+        def torch_tail():
+            a = torch.nn.functional.layer_norm(hx.float(), (co,), gm, bt, 1e-6).to(torch.bfloat16)
+            a = torch.nn.functional.silu(torch.nn.functional.linear(a, w1, b1.to(torch.bfloat16)))
+            return torch.nn.functional.linear(a, w2, b2.to(torch.bfloat16)) + xx
+        t_t = timed(torch_tail, 5)
+        tail = {"rows": n, "C": co, "fused_ms": round(t_f, 4), "torch_ms": round(t_t, 4),
+                "fused_GBps": round(3 * n * co * 2 / (t_f * 1e-3) / 1e9, 1),
+                "fused_TFLOPs": round(16 * n * co * co / (t_f * 1e-3) / 1e12, 1)}
+        del hx, xx, yt
+
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -274,7 +297,7 @@ def main():
         "extras": {"mvox_per_s": round(mvox, 2), "compulsory_GBps": round(gbs, 1),
                    "kmap_build_ms": round(float(np.median(map_ms)), 4), "coord_gen_s": round(gen_s, 2),
                    "executed_over_active_pairs": round(executed_pairs / max(P, 1), 4), "skip_group_rows": gsz, "wall_s": round(wall, 3),
-                   "upsample_block_e2e": e2e, "measured_peaks": measured},
+                   "upsample_block_e2e": e2e, "convnext_tail": tail, "measured_peaks": measured},
     }
     print(json.dumps(out), flush=True)
 

@@ -84,6 +84,17 @@ int spc_subm_conv_gathered(const void* x_src, int64_t M, const int32_t* row_map,
 int spc_gather_ln_act(const void* x_src, int64_t M, int C, const int32_t* row_map, int shift, const float* gamma,
                       const float* beta, float eps, int act, int dtype, int64_t N, void* out);
 
+/* ConvNeXt tail in one pass: y = x + W2 silu(W1 (LayerNorm(h) * gamma + beta) + b1) + b2 per row, fp32 statistics
+ * and accumulation, the hidden activations rounded to `dtype` between the two products, one rounding of y.
+ * h, x, y [N,C], w1 [4C,C], w2 [C,4C] (torch Linear layout): `dtype` (SPC_F16/SPC_BF16), 16-byte aligned;
+ * gamma, beta, b2 [C] and b1 [4C]: `param_dtype` or NULL (gamma 1, others 0); C = 64, 128 or 256.
+ * y may alias h or x.
+ * Replaces: the tail of SDecoder::convnext after its conv -- layer_norm, linear, act_ SILU, linear, add_
+ * (src/sdec.cu:60-66, src/ops.cu:30-75, src/gemm.cu:24-63). */
+int spc_convnext_mlp(const void* h, const void* x, const void* gamma, const void* beta, float eps, const void* w1,
+                     const void* b1, const void* w2, const void* b2, int dtype, int param_dtype, int64_t N, int C,
+                     void* y);
+
 /* Skip connection of the upsample block, in place: h[i,c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep] with
  * rep = Co / (Cin/8), the fp32 sum rounded once to `dtype` (bit-identical to the reference); h [m,Co], x [n,Cin],
  * both SPC_F16 or SPC_BF16, 16-byte aligned; Cin % 8 == 0, Co % 8 == 0, Co % (Cin/8) == 0. src entries outside

@@ -143,6 +143,26 @@ SPC_API int spc_gather_ln_act(const void* x_src, int64_t M, int C, const int32_t
   });
 }
 
+SPC_API int spc_convnext_mlp(const void* h, const void* x, const void* gamma, const void* beta, float eps,
+                             const void* w1, const void* b1, const void* w2, const void* b2, int dtype,
+                             int param_dtype, int64_t N, int C, void* y) {
+  return guarded([&] {
+    REQ(N >= 0 && C > 0, "N=%lld C=%d", (long long)N, C);
+    DT dt = float_dt(dtype, "h/x/w"), pdt = float_dt(param_dtype, "gamma/beta/b1/b2");
+    REQ(dt != F32, "h/x/w must be fp16 or bf16");
+    if (N == 0) return;
+    REQ(h && x && w1 && w2 && y, "null h/x/w1/w2/y");
+    Tensor th = borrow(h, {N, C}, dt), tx = borrow(x, {N, C}, dt), ty = borrow(y, {N, C}, dt);
+    Tensor tw1 = borrow(w1, {4 * (i64)C, C}, dt), tw2 = borrow(w2, {C, 4 * (i64)C}, dt), tg, tb, tb1, tb2;
+    if (gamma) tg = borrow(gamma, {C}, pdt);
+    if (beta) tb = borrow(beta, {C}, pdt);
+    if (b1) tb1 = borrow(b1, {4 * (i64)C}, pdt);
+    if (b2) tb2 = borrow(b2, {C}, pdt);
+    convnext_mlp(th, tx, gamma ? &tg : nullptr, beta ? &tb : nullptr, eps, tw1, b1 ? &tb1 : nullptr, tw2,
+                 b2 ? &tb2 : nullptr, ty);
+  });
+}
+
 SPC_API int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, int Co, int64_t n, int Cin,
                          int dtype) {
   return guarded([&] {

@@ -1,0 +1,340 @@
+// ConvNeXt tail of the sparse decoder in one kernel (reference SDecoder::convnext after its conv, src/sdec.cu:59-67):
+//
+//   y = x + W2 · silu(W1 · (LayerNorm(h) * gamma + beta) + b1) + b2        (per row; hidden width 4C)
+//
+// which the reference runs as layer_norm (f32 casts, src/ops.cu:30-75), linear (src/gemm.cu:24-63), act_ SILU,
+// linear, add_ -- about ten passes over rows of C and 4C channels. Here each row is read once (h and x) and written
+// once (y); the 4C-wide hidden activations never leave registers.
+//
+// Work split. A workgroup of 4 wavefronts walks row tiles (persistent grid); each wavefront owns R blocks of 32 rows.
+// The hidden dimension is processed in chunks of 32:
+//   GEMM1  H^T[32 hid x 32 rows] = W1[chunk rows, :] · Xn^T      (C/16 v_mfma_f32_32x32x16, K = channels)
+//   H^T    += b1, SiLU, rounded to the operand type
+//   GEMM2  Y^T[C x 32 rows]    += W2[:, chunk] · H^T            (2 MFMAs per 32 output channels)
+// MFMA 32x32x16 layouts: lane l supplies A row l%32 and B column l%32 with K values (l/32)*8 .. +8; the result gives
+// lane l column l%32 and rows (i/4)*8 + (l/32)*4 + i%4. So a lane's normalized row chunks (row l%32, channels
+// t*16 + (l/32)*8 .. +8) are GEMM1's B operand as loaded, and GEMM1's result (column = row l%32, hidden rows
+// (i/4)*8 + (l/32)*4 + i%4) is GEMM2's B operand without any transpose, provided W2's K order is permuted to match;
+// the weight pack below stores W1 and W2 in exactly those operand orders, one 16-byte load per lane per MFMA.
+// Weights live in LDS: all of them for C = 64 (64 KiB, loaded once per workgroup), else streamed per chunk through
+// three chunk buffers shared by the 4 wavefronts.
+#include "spconv.h"
+
+namespace {
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+constexpr uint32_t kOOR = 0xffff0000u;
+
+template <bool F16>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                   0);
+}
+template <bool F16>
+__device__ __forceinline__ float lo(uint32_t v) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)v);
+  else return __uint_as_float(v << 16);
+}
+template <bool F16>
+__device__ __forceinline__ float hi(uint32_t v) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+  else return __uint_as_float(v & 0xffff0000u);
+}
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (F16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+__device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
+template <int C>
+struct MlpShape {
+  static constexpr int NCH = C / 8;                // hidden chunks of 32 (hidden width 4C)
+  static constexpr int KS = C / 16;                // GEMM1 K steps per chunk
+  static constexpr int YT = C / 32;                // 32-channel output tiles
+  static constexpr int W1Q = KS * 64;              // 16-byte units of a chunk's W1 part
+  static constexpr int CHUNK = W1Q + YT * 2 * 64;  // 16-byte units per chunk (W1 then W2)
+  static constexpr bool RESIDENT = C == 64;        // all weights in LDS (NCH * CHUNK * 16 = 64 KiB)
+  static constexpr int LDSQ = RESIDENT ? NCH * CHUNK : 3 * CHUNK;
+};
+
+// Weights into operand order: wp[chunk][W1: KS x 64 lanes | W2: YT x 2 x 64 lanes] 16-byte units.
+//   W1 unit (t, lane): hidden chunk*32 + lane%32, channels t*16 + (lane/32)*8 .. +8             (w1 [4C, C])
+//   W2 unit (tt, u, lane): output channel tt*32 + lane%32, hidden chunk*32 + u*16 + (lane/32)*4 + {0..3, 8..11}
+//                                                                                             (w2 [C, 4C])
+template <int C>
+__global__ void k_pack_mlp(const uint16_t* __restrict__ w1, const uint16_t* __restrict__ w2, u32x4* __restrict__ wp) {
+  using S = MlpShape<C>;
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= S::NCH * S::CHUNK) return;
+  const int c = q / S::CHUNK, k = q % S::CHUNK, lane = k & 63;
+  if (k < S::W1Q) {
+    const int t = k >> 6;
+    wp[q] = *(const u32x4*)&w1[(i64)(c * 32 + (lane & 31)) * C + t * 16 + (lane >> 5) * 8];
+  } else {
+    const int k2 = k - S::W1Q, u = (k2 >> 6) & 1, tt = k2 >> 7;
+    const uint16_t* r = &w2[(i64)(tt * 32 + (lane & 31)) * (4 * C) + c * 32 + u * 16 + (lane >> 5) * 4];
+    const u32x2 a = *(const u32x2*)r, b = *(const u32x2*)(r + 8);
+    wp[q] = u32x4{a[0], a[1], b[0], b[1]};
+  }
+}
+
+__global__ void k_params_f32(const void* p, int dt, int n, float dflt, float* o) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if (!p) o[i] = dflt;
+  else if (dt == F32) o[i] = ((const float*)p)[i];
+  else {
+    const uint16_t v = ((const uint16_t*)p)[i];
+    o[i] = dt == BF16 ? __uint_as_float((uint32_t)v << 16) : (float)__builtin_bit_cast(_Float16, v);
+  }
+}
+
+// params: f32 [gamma C | beta C | b1 4C | b2 C]
+template <bool F16, int C, int R, int NW, bool XE>
+__global__ void __launch_bounds__(NW * 64) k_convnext_mlp(const uint16_t* h, const uint16_t* x,
+                                                      uint16_t* y, const u32x4* __restrict__ wp,
+                                                      const float* __restrict__ params, float eps, i64 n, i64 tiles,
+                                                      uint32_t h_bytes, uint32_t x_bytes, uint32_t y_bytes) {
+  using S = MlpShape<C>;
+  __shared__ u32x4 lw[S::LDSQ];
+  __shared__ float lp[7 * C];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r32 = lane & 31, h8 = lane >> 5;
+  const float* s_g = lp;
+  const float* s_bt = lp + C;
+  const float* s_b1 = lp + 2 * C;
+  const float* s_b2 = lp + 6 * C;
+  for (int i = tid; i < 7 * C; i += NW * 64) lp[i] = params[i];
+  if constexpr (S::RESIDENT)
+    for (int i = tid; i < S::LDSQ; i += NW * 64) lw[i] = wp[i];
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(h), 0, (int)h_bytes,
+                                                                      0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, (int)x_bytes,
+                                                                      0x00020000);
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(y, 0, (int)y_bytes, 0x00020000);
+  constexpr int SQ = (S::CHUNK + NW * 64 - 1) / (NW * 64);  // staged 16-byte units per thread per chunk (streaming mode)
+
+  for (i64 tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const i64 row0 = tile * (NW * R * 32) + (i64)wave * (R * 32);
+    asm volatile("" ::: "memory");  // keeps the per-channel LDS parameter reads inside the loop (no 100-VGPR hoist)
+    // rows of h (LayerNorm input) as GEMM1 B operands, and x (residual) in the output layout (here when XE, else in
+    // the epilogue)
+    u32x4 xn[R][S::KS];
+    u32x2 xr[R][S::YT][4];
+#pragma unroll
+    for (int rb = 0; rb < R; rb++) {
+      const i64 row = row0 + rb * 32 + r32;
+      const bool ok = row < n;
+#pragma unroll
+      for (int t = 0; t < S::KS; t++)
+        xn[rb][t] = __builtin_amdgcn_raw_buffer_load_b128(rh, ok ? (uint32_t)((row * C + t * 16 + h8 * 8) * 2) : kOOR,
+                                                          0, 0);
+      if constexpr (XE)
+#pragma unroll
+        for (int tt = 0; tt < S::YT; tt++)
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+            xr[rb][tt][g] = __builtin_amdgcn_raw_buffer_load_b64(
+                rx, ok ? (uint32_t)((row * C + tt * 32 + g * 8 + h8 * 4) * 2) : kOOR, 0, 0);
+    }
+    // LayerNorm: a row's C values sit in lanes r32 and r32 + 32; mean first, then the centred variance
+#pragma unroll
+    for (int rb = 0; rb < R; rb++) {
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < S::KS; t++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) s += lo<F16>(xn[rb][t][j]) + hi<F16>(xn[rb][t][j]);
+      s += __shfl_xor(s, 32, 64);
+      const float mean = s * (1.0f / C);
+      float q = 0.f;
+#pragma unroll
+      for (int t = 0; t < S::KS; t++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float a = lo<F16>(xn[rb][t][j]) - mean, b = hi<F16>(xn[rb][t][j]) - mean;
+          q += a * a + b * b;
+        }
+      q += __shfl_xor(q, 32, 64);
+      const float rstd = rsqrtf(q * (1.0f / C) + eps);
+#pragma unroll
+      for (int t = 0; t < S::KS; t++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int ch = t * 16 + h8 * 8 + 2 * j;
+          const float a = (lo<F16>(xn[rb][t][j]) - mean) * rstd * s_g[ch] + s_bt[ch];
+          const float b = (hi<F16>(xn[rb][t][j]) - mean) * rstd * s_g[ch + 1] + s_bt[ch + 1];
+          xn[rb][t][j] = pack2<F16>(a, b);
+        }
+    }
+
+    f32x16 acc[R][S::YT];
+#pragma unroll
+    for (int rb = 0; rb < R; rb++)
+#pragma unroll
+      for (int tt = 0; tt < S::YT; tt++) acc[rb][tt] = f32x16{};
+
+    // Software pipeline over hidden chunks: GEMM1 of chunk c+1 is issued before the SiLU of chunk c, so the VALU
+    // work overlaps MFMA execution. Streaming mode keeps three chunk buffers: in iteration c the wavefronts read
+    // W1 of chunk c+1 and W2 of chunk c, and chunk c+2 is written into the buffer of chunk c-1.
+    auto buf = [&](int c) -> const u32x4* { return S::RESIDENT ? lw + c * S::CHUNK : lw + (c % 3) * S::CHUNK; };
+    auto gemm1 = [&](const u32x4* cw, f32x16 (&hacc)[R]) {
+#pragma unroll
+      for (int rb = 0; rb < R; rb++) hacc[rb] = f32x16{};
+#pragma unroll
+      for (int t = 0; t < S::KS; t++) {
+        const u32x4 a = cw[t * 64 + lane];
+#pragma unroll
+        for (int rb = 0; rb < R; rb++) hacc[rb] = mfma32<F16>(a, xn[rb][t], hacc[rb]);
+      }
+    };
+    u32x4 stg[SQ];
+    if constexpr (!S::RESIDENT) {  // chunks 0 and 1 into buffers 0 and 1, once every wavefront left the last tile
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 2 * SQ; k++)
+        if ((k % SQ) * NW * 64 + tid < S::CHUNK)
+          lw[(k / SQ) * S::CHUNK + (k % SQ) * NW * 64 + tid] = wp[(k / SQ) * S::CHUNK + (k % SQ) * NW * 64 + tid];
+      __syncthreads();
+    }
+    f32x16 hnext[R];
+    gemm1(buf(0), hnext);
+#pragma unroll 1
+    for (int c = 0; c < S::NCH; c++) {
+      if constexpr (!S::RESIDENT)
+        if (c + 2 < S::NCH)
+#pragma unroll
+          for (int k = 0; k < SQ; k++)
+            if (k * NW * 64 + tid < S::CHUNK) stg[k] = wp[(c + 2) * S::CHUNK + k * NW * 64 + tid];
+      f32x16 hacc[R];
+#pragma unroll
+      for (int rb = 0; rb < R; rb++) hacc[rb] = hnext[rb];
+      if (c + 1 < S::NCH) gemm1(buf(c + 1), hnext);
+      u32x4 hb[R][2];
+#pragma unroll
+      for (int rb = 0; rb < R; rb++)
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int i = u * 8 + 2 * j;  // accumulators i, i+1: hidden rows (i/4)*8 + h8*4 + i%4 (+1)
+            const int hid = c * 32 + (i >> 2) * 8 + h8 * 4 + (i & 3);
+            hb[rb][u][j] = pack2<F16>(silu(hacc[rb][i] + s_b1[hid]), silu(hacc[rb][i + 1] + s_b1[hid + 1]));
+          }
+      const u32x4* cw = buf(c);
+#pragma unroll
+      for (int tt = 0; tt < S::YT; tt++)
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          const u32x4 a = cw[S::W1Q + (tt * 2 + u) * 64 + lane];
+#pragma unroll
+          for (int rb = 0; rb < R; rb++) acc[rb][tt] = mfma32<F16>(a, hb[rb][u], acc[rb][tt]);
+        }
+      // buffer (c+2) % 3 held chunk c-1, last read in iteration c-1, which every wavefront finished before the
+      // barrier that ended it; one barrier per chunk publishes the new contents
+      if constexpr (!S::RESIDENT)
+        if (c + 2 < S::NCH) {
+#pragma unroll
+          for (int k = 0; k < SQ; k++)
+            if (k * NW * 64 + tid < S::CHUNK) lw[((c + 2) % 3) * S::CHUNK + k * NW * 64 + tid] = stg[k];
+          __syncthreads();
+        }
+    }
+    // y = x + acc + b2, 4 consecutive channels per (tile, group) as one 8-byte store; rows past n are dropped
+#pragma unroll
+    for (int rb = 0; rb < R; rb++) {
+      const i64 row = row0 + rb * 32 + r32;
+      const bool ok = row < n;
+      if constexpr (!XE)  // wide rows: the residual is requested only now, which saves its registers in the loop
+#pragma unroll
+        for (int tt = 0; tt < S::YT; tt++)
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+            xr[rb][tt][g] = __builtin_amdgcn_raw_buffer_load_b64(
+                rx, ok ? (uint32_t)((row * C + tt * 32 + g * 8 + h8 * 4) * 2) : kOOR, 0, 0);
+#pragma unroll
+      for (int tt = 0; tt < S::YT; tt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int co = tt * 32 + g * 8 + h8 * 4;
+          const u32x2 xv = xr[rb][tt][g];
+          const float v0 = acc[rb][tt][g * 4 + 0] + s_b2[co + 0] + lo<F16>(xv[0]);
+          const float v1 = acc[rb][tt][g * 4 + 1] + s_b2[co + 1] + hi<F16>(xv[0]);
+          const float v2 = acc[rb][tt][g * 4 + 2] + s_b2[co + 2] + lo<F16>(xv[1]);
+          const float v3 = acc[rb][tt][g * 4 + 3] + s_b2[co + 3] + hi<F16>(xv[1]);
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2<F16>(v0, v1), pack2<F16>(v2, v3)}, ry,
+                                                ok ? (uint32_t)((row * C + co) * 2) : kOOR, 0, 0);
+        }
+    }
+  }
+}
+
+int cus() {
+  static int n = [] {
+    int dev = 0, v = 0;
+    CK(hipGetDevice(&dev));
+    CK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
+    return v;
+  }();
+  return n;
+}
+
+template <bool F16, int C, int R, int NW, bool XE>
+void launch_mlp(const Tensor& h, const Tensor& x, const Tensor& w1, const Tensor& w2, const Tensor& params, float eps,
+                Tensor& y) {
+  using S = MlpShape<C>;
+  const i64 n = h.size(0);
+  Tensor wp = empty({(i64)S::NCH * S::CHUNK * 8}, h.dt);
+  k_pack_mlp<C><<<cdiv(S::NCH * S::CHUNK, 256), 256, 0, stream()>>>(w1.ptr<uint16_t>(), w2.ptr<uint16_t>(),
+                                                                      (u32x4*)wp.p);
+  const i64 tiles = cdiv(n, (i64)NW * R * 32);
+  const i64 grid = std::min<i64>(tiles, (i64)cus() * 2);
+  k_convnext_mlp<F16, C, R, NW, XE><<<(unsigned)grid, NW * 64, 0, stream()>>>(
+      h.ptr<uint16_t>(), x.ptr<uint16_t>(), y.ptr<uint16_t>(), (const u32x4*)wp.p, params.ptr<float>(), eps, n, tiles,
+      (uint32_t)h.bytes(), (uint32_t)x.bytes(), (uint32_t)y.bytes());
+}
+}  // namespace
+
+void convnext_mlp(const Tensor& h, const Tensor& x, const Tensor* gamma, const Tensor* beta, float eps, const Tensor& w1,
+                  const Tensor* b1, const Tensor& w2, const Tensor* b2, Tensor& y) {
+  REQ(h.dim() == 2 && (h.dt == BF16 || h.dt == F16), "h must be bf16/fp16 [N,C]");
+  const i64 n = h.size(0);
+  const int C = (int)h.size(1);
+  REQ(C == 64 || C == 128 || C == 256, "C=%d: the fused tail supports C = 64, 128, 256", C);
+  REQ(x.dt == h.dt && x.dim() == 2 && x.size(0) == n && x.size(1) == C, "x must match h");
+  REQ(y.dt == h.dt && y.dim() == 2 && y.size(0) == n && y.size(1) == C, "y must match h");
+  REQ(w1.dt == h.dt && w1.dim() == 2 && w1.size(0) == 4 * C && w1.size(1) == C, "w1 must be [4C, C] of h's dtype");
+  REQ(w2.dt == h.dt && w2.dim() == 2 && w2.size(0) == C && w2.size(1) == 4 * C, "w2 must be [C, 4C] of h's dtype");
+  for (const Tensor* t : {gamma, beta, b2}) REQ(!t || t->numel() == C, "gamma/beta/b2 must have C elements");
+  REQ(!b1 || b1->numel() == 4 * C, "b1 must have 4C elements");
+  REQ((uint64_t)h.bytes() <= 0xfffe0000ull && (uint64_t)x.bytes() <= 0xfffe0000ull, "h/x larger than 4 GiB");
+  REQ(((uintptr_t)h.p | (uintptr_t)x.p | (uintptr_t)y.p | (uintptr_t)w1.p | (uintptr_t)w2.p) % 16 == 0,
+      "h, x, y, w1, w2 must be 16-byte aligned");
+  if (n == 0) return;
+  Tensor params = empty({7 * (i64)C}, F32);
+  float* pp = params.ptr<float>();
+  auto conv = [&](const Tensor* t, int off, int cnt, float dflt) {
+    k_params_f32<<<cdiv(cnt, 256), 256, 0, stream()>>>(t ? t->p : nullptr, t ? (int)t->dt : F32, cnt, dflt, pp + off);
+  };
+  conv(gamma, 0, C, 1.f);
+  conv(beta, C, C, 0.f);
+  conv(b1, 2 * C, 4 * C, 0.f);
+  conv(b2, 6 * C, C, 0.f);
+  const bool f16 = h.dt == F16;
+  // measured on the MI355X (2.2 M / 0.8 M / 0.4 M rows): two 32-row blocks per wavefront halve the LDS weight
+  // reads at C = 128; at C = 256 the residual is loaded in the epilogue to stay clear of spills
+  if (C == 64) f16 ? launch_mlp<true, 64, 1, 4, true>(h, x, w1, w2, params, eps, y) : launch_mlp<false, 64, 1, 4, true>(h, x, w1, w2, params, eps, y);
+  else if (C == 128) f16 ? launch_mlp<true, 128, 2, 4, true>(h, x, w1, w2, params, eps, y) : launch_mlp<false, 128, 2, 4, true>(h, x, w1, w2, params, eps, y);
+  else f16 ? launch_mlp<true, 256, 1, 4, false>(h, x, w1, w2, params, eps, y) : launch_mlp<false, 256, 1, 4, false>(h, x, w1, w2, params, eps, y);
+  CK(hipGetLastError());
+}

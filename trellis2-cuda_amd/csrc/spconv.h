@@ -73,6 +73,14 @@ void subm_conv_gathered(const Tensor& x_src, const Tensor& row_map, int shift, c
 void gather_ln_act(const Tensor& x_src, const Tensor* row_map, int shift, const Tensor* gamma, const Tensor* beta,
                    float eps, int act, Tensor& out);
 
+// ConvNeXt tail of the decoder in one pass (reference SDecoder::convnext after its conv, src/sdec.cu:60-66):
+// y = x + W2 silu(W1 (LayerNorm(h) * gamma + beta) + b1) + b2 per row, LayerNorm eps as given, fp32 accumulation,
+// hidden activations rounded to h's dtype between the two products. h, x, y [N,C] and w1 [4C,C], w2 [C,4C] of one
+// dtype (fp16/bf16); gamma, beta, b2 [C] and b1 [4C] of any float dtype or null; C = 64, 128 or 256. y may alias h
+// or x.
+void convnext_mlp(const Tensor& h, const Tensor& x, const Tensor* gamma, const Tensor* beta, float eps, const Tensor& w1,
+                  const Tensor* b1, const Tensor& w2, const Tensor* b2, Tensor& y);
+
 // Skip connection of the upsample block, in place (reference k_add_skip, src/sdec.cu:38-43):
 // h[i, c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep], rep = Co / (Cin/8), fp32 sum rounded once (bit-identical
 // to the reference). h [m,Co] and x [n,Cin] of one dtype (fp16/bf16); entries of src outside x leave the row.

@@ -26,7 +26,8 @@ EMPTY = 0xFFFFFFFF
 # the C ABI's exported symbols (every declaration of include/spconv_amd.h)
 SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_cache_free", "spc_cache_info",
            "spc_cache_valid", "spc_conv_cfg", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
-           "spc_gather_ln_act", "spc_add_skip", "spc_subdivide")
+           "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp",
+           "spc_subdivide")
 
 _lib = None
 
@@ -54,6 +55,7 @@ def load_library():
     L.spc_subm_conv_gathered.argtypes = [P, I64, P, I, P, P, P, I, I, I, I, I, I64, I, I, P, P]
     L.spc_gather_ln_act.argtypes = [P, I64, I, P, I, P, P, ctypes.c_float, I, I, I64, P]
     L.spc_add_skip.argtypes = [P, P, P, I64, I, I64, I, I]
+    L.spc_convnext_mlp.argtypes = [P, P, P, P, ctypes.c_float, P, P, P, P, I, I, I64, I, P]
     L.spc_subdivide.argtypes = [P, P, I64, P, P, ctypes.POINTER(I64)]
     for name in SYMBOLS:
         if name != "spc_last_error":
@@ -227,6 +229,25 @@ def gather_ln_act(x_src, row_map=None, shift: int = 0, gamma=None, beta=None, ep
         out = torch.empty((N, C), dtype=x_src.dtype, device=x_src.device)
     _check(load_library().spc_gather_ln_act(_ptr(x_src), M, C, _ptr(row_map), shift, _ptr(gamma), _ptr(beta),
                                             eps, act, _dt(x_src), N, _ptr(out)))
+    return out
+
+
+def convnext_mlp(h, x, gamma, beta, w1, b1, w2, b2, eps: float = 1e-6, out=None):
+    """x + W2 silu(W1 (LayerNorm(h) * gamma + beta) + b1) + b2 in one pass (the tail of the reference's
+    SDecoder::convnext after its conv, src/sdec.cu:60-66). w1 [4C, C], w2 [C, 4C] in h's dtype; gamma, beta, b1, b2
+    share one float dtype (or are None). out may be h or x."""
+    N, C = h.shape
+    ps = [p for p in (gamma, beta, b1, b2) if p is not None]
+    if any(p.dtype != ps[0].dtype for p in ps):
+        raise ValueError("gamma, beta, b1, b2 must share one dtype")
+    for name, t in (("x", x), ("w1", w1), ("w2", w2)):
+        if t.dtype != h.dtype:
+            raise ValueError(f"{name} must have h's dtype {h.dtype}")
+    if out is None:
+        out = _torch().empty_like(h)
+    _check(load_library().spc_convnext_mlp(_ptr(h), _ptr(x), _ptr(gamma), _ptr(beta), eps, _ptr(w1), _ptr(b1),
+                                           _ptr(w2), _ptr(b2), _dt(h), _dt(ps[0]) if ps else F32, N, C,
+                                           _ptr(out)))
     return out
 
 
