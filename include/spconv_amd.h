@@ -20,6 +20,10 @@ extern "C" {
 
 enum { SPC_F32 = 0, SPC_F16 = 1, SPC_BF16 = 2 };
 enum { SPC_ACT_NONE = 0, SPC_ACT_SILU = 1 };
+/* Or'ed into a conv's act: the reference's fp16 rounding sequence instead of one rounding -- y = f16(f16(acc) + b),
+ * then y = f16(y / (1 + exp(-y))) for SiLU, then y = f16(y + residual) (src/spconv.cu:141-143, src/ops.cu:79-82,
+ * 105-113). x, w, out fp16; bias and residual fp16 or NULL. */
+enum { SPC_EPI_F16_COMPAT = 256 };
 #define SPC_EMPTY 0xffffffffu
 
 typedef struct spc_cache spc_cache; /* owns one SpConvCache (reference src/spconv.h:6-11) */
@@ -53,6 +57,13 @@ int spc_cache_valid(spc_cache* c, int B1, const int32_t** list, const int32_t** 
 /* Tile choice for an (N, Ci, Co) conv: rows per tile/schedule block B1, channels per K stage BK, split S.
  * Replaces: spconv_cfg (src/spconv.h:13-14, src/spconv.cu:177-221); the tile table is fixed per width. */
 int spc_conv_cfg(int64_t N, int Ci, int Co, int* B1, int* BK, int* S);
+
+/* The reference's tile choice replayed from a FlexGEMM autotune cache file (`path`, device section `device`, e.g.
+ * "NVIDIA H200"): split S from the splitk table, then B1/BK for (floor(log2 N), Ci, Co, S); 128/64/1 where the file
+ * has no entry. Host only (no GPU needed); the file is parsed once per (path, device). This build's kernels keep their
+ * own tiles; B1 here gives the reference's schedule blocks for spc_cache_valid.
+ * Replaces: spconv_cfg's table replay (src/spconv.cu:176-221). */
+int spc_conv_cfg_autotune(const char* path, const char* device, int64_t N, int Ci, int Co, int* B1, int* BK, int* S);
 
 /* out[N,Co] (dtype = x's) = subm_conv3d(x [N,Ci], w [Co,27,Ci], b [Co] or NULL).
  * x and w: both SPC_F16 or both SPC_BF16; b_dtype: SPC_F32/F16/BF16. Ci % 32 == 0, Co % 64 == 0.

@@ -212,3 +212,46 @@ def test_gathered_conv(gpu, ci, co):
         nbr, _, _, _ = oracle.build_neighbors(ch.cpu().numpy())
         ref = oracle.conv(xg.float().cpu().numpy(), qw, b, nbr, res=qr, act=act)
         compare(y1, ref, "f32", f"gathered ci={ci} co={co} act={act}")
+
+
+@pytest.mark.parametrize("ci,co", [(64, 64), (64, 128), (256, 256), (128, 192)])
+def test_f16_compat_epilogue(gpu, ci, co):
+    """EPI_F16_COMPAT reproduces the reference's rounding sequence on the kernel's own fp32 sums: f16(f16(acc) + b),
+    then SiLU rounded to f16, then the residual add rounded to f16. Checked against that sequence applied on the host
+    to the same kernel's fp32 output without bias: bit-exact without SiLU; with SiLU the host exp may differ from
+    the device's in the last fp32 bit, so at most 1e-3 of the elements may differ, by one fp16 ulp (plus, after a residual
+    add, one ulp of the SiLU value that differed)."""
+    c = shell(7.0)
+    n = len(c)
+    print(f"compat case n={n} ci={ci} co={co}", flush=True)
+    w, b = W.conv_params(W.Config("t", 0, 0, (0, 0), False, 0, ci, co, "f16", "", 31))
+    tx, _ = quantize(W.features(n, ci, 8), "f16")
+    tw, _ = quantize(w, "f16")
+    tb, _ = quantize(b * 10, "f16")
+    tr, _ = quantize(W.features(n, co, 9), "f16")
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    xs, ws, bs, rs = tx.to(gpu), tw.to(gpu), tb.to(gpu), tr.to(gpu)
+    acc = sp.subm_conv_fused(xs, ws, None, cache, out_dtype=torch.float32).cpu()
+    for act in (0, 1):
+        for res in (None, rs):
+            y = sp.subm_conv_fused(xs, ws, bs, cache, residual=res, act=act | sp.EPI_F16_COMPAT).cpu()
+            e = (acc.half().float() + tb.float()).half().float()
+            if act:
+                e = (e.double() / (1 + torch.exp(-e.double()))).float().half().float()
+            s = e.clone()  # the SiLU value: a one-ulp difference there survives the residual add
+            if res is not None:
+                e = e + tr.float()
+            e = e.half()
+            what = f"ci={ci} co={co} act={act} res={res is not None}"
+            assert y.dtype == torch.float16, what
+            if not act:
+                assert torch.equal(y, e), what
+            else:
+                d = (y.float() - e.float()).abs()
+                bad = d > 0
+                what += f": {int(bad.sum())} of {bad.numel()} differ, max {float(d.max()):.3g}"
+                assert bad.float().mean() <= 1e-3, what
+                tol = ulp(e.float()[bad].numpy(), "f16") + (ulp(s[bad].numpy(), "f16") if res is not None else 0)
+                assert torch.all(d[bad] <= torch.from_numpy(tol)), what
+    with pytest.raises(RuntimeError):  # bf16 is not a compat dtype
+        sp.subm_conv_fused(xs.bfloat16(), ws.bfloat16(), None, cache, act=sp.EPI_F16_COMPAT)

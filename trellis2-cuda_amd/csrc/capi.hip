@@ -176,6 +176,18 @@ SPC_API int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, 
   });
 }
 
+SPC_API int spc_conv_cfg_autotune(const char* path, const char* device, int64_t N, int Ci, int Co, int* B1, int* BK,
+                                  int* S) {
+  return guarded([&] {
+    REQ(path && device && B1 && BK && S, "null argument");
+    REQ(N >= 0 && Ci > 0 && Co > 0, "N=%lld Ci=%d Co=%d", (long long)N, Ci, Co);
+    const SpConvCfg c = spconv_cfg_autotune(path, device, N, Ci, Co);
+    *B1 = c.B1;
+    *BK = c.BK;
+    *S = c.S;
+  });
+}
+
 SPC_API int spc_subm_conv(const void* x, const void* w, const void* b, int dtype, int b_dtype, int64_t N, int Ci,
                           int Co, spc_cache* c, void* out) {
   return spc_subm_conv_fused(x, w, b, nullptr, dtype, b_dtype, SPC_F32, dtype, SPC_ACT_NONE, N, Ci, Co, c, out);

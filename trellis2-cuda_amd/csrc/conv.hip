@@ -88,6 +88,9 @@ __device__ __forceinline__ void wg_barrier() {
 // SiLU with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each). Large negative v gives
 // exp -> inf, rcp -> 0 and a signed zero, as v / (1 + exp(-v)) does.
 __device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+// fp16-compatible epilogue helpers: round to fp16 and back; SiLU with the IEEE quotient and the accurate exp
+__device__ __forceinline__ float f16r(float v) { return (float)(_Float16)v; }
+__device__ __forceinline__ float silu_ieee(float v) { return v / (1.0f + expf(-v)); }
 
 struct ConvArgs {
   const uint16_t* x;
@@ -236,9 +239,16 @@ __global__ void __launch_bounds__(WGM* WGN * 64) k_conv(ConvArgs a) {
         int r = row0 + wm * WTM + i * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
         if (r >= N) continue;
         i64 o = (i64)a.order[r] * a.Co + co;
-        float v = acc[i][j][e] + bv;
-        if (a.act == ACT_SILU) v = silu(v);
-        if (a.res) v += load_elem(a.res, o, a.res_dt);
+        float v;
+        if (a.act & EPI_F16_COMPAT) {
+          v = f16r(f16r(acc[i][j][e]) + bv);
+          if ((a.act & ~EPI_F16_COMPAT) == ACT_SILU) v = f16r(silu_ieee(v));
+          if (a.res) v = f16r(v + load_elem(a.res, o, a.res_dt));
+        } else {
+          v = acc[i][j][e] + bv;
+          if (a.act == ACT_SILU) v = silu(v);
+          if (a.res) v += load_elem(a.res, o, a.res_dt);
+        }
         store_elem(a.out, o, a.out_dt, v);
       }
     }
@@ -272,7 +282,7 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 struct Epi {
   __amdgpu_buffer_rsrc_t out, res;
   int out_dt, res_dt;  // res_dt < 0: no residual
-  bool silu;
+  bool silu, compat;   // compat: the fp16 rounding sequence (EPI_F16_COMPAT)
 };
 __device__ __forceinline__ Epi make_epi(const ConvArgs& a) {
   Epi e;
@@ -280,7 +290,8 @@ __device__ __forceinline__ Epi make_epi(const ConvArgs& a) {
   e.res = make_rsrc(a.res, a.res_bytes);
   e.out_dt = a.out_dt;
   e.res_dt = a.res ? a.res_dt : -1;
-  e.silu = a.act == ACT_SILU;
+  e.silu = (a.act & ~EPI_F16_COMPAT) == ACT_SILU;
+  e.compat = (a.act & EPI_F16_COMPAT) != 0;
   return e;
 }
 
@@ -299,6 +310,18 @@ __device__ __forceinline__ void load_res8(const Epi& e, uint32_t o, bool ok, u32
 // out[o .. o+8) = act(v + bias) [+ residual r], one rounding to the output dtype
 __device__ __forceinline__ void store_row8(const Epi& e, uint32_t o, bool ok, float (&v)[8], const float (&bias8)[8],
                                            const u32x4 (&r)[2]) {
+  if (e.compat) {  // fp16 x/out/bias/residual (checked on the host)
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      v[q] = f16r(f16r(v[q]) + bias8[q]);
+      if (e.silu) v[q] = f16r(silu_ieee(v[q]));
+      if (e.res_dt == F16) v[q] = v[q] + f16_to_f32((uint16_t)(r[0][q >> 1] >> ((q & 1) * 16)));
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{pack2<false>(v[0], v[1]), pack2<false>(v[2], v[3]),
+                                                 pack2<false>(v[4], v[5]), pack2<false>(v[6], v[7])},
+                                           e.out, ok ? o * 2u : kOutOfRange, 0, 0);
+    return;
+  }
 #pragma unroll
   for (int q = 0; q < 8; q++) v[q] += bias8[q];
   if (e.silu) {
@@ -1184,7 +1207,11 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   REQ(Ci > 0 && Ci % 32 == 0 && Ci <= kMaxCi, "Ci=%d must be a multiple of 32 (at most %d)", Ci, kMaxCi);
   REQ(Co > 0 && Co % 64 == 0, "Co=%d must be a multiple of 64", Co);
   REQ(N == c.N, "x has %d rows, neighbour cache %d", N, c.N);
-  REQ(act == ACT_NONE || act == ACT_SILU, "act=%d", act);
+  const int act0 = act & ~EPI_F16_COMPAT;
+  REQ(act0 == ACT_NONE || act0 == ACT_SILU, "act=%d", act);
+  if (act & EPI_F16_COMPAT)
+    REQ(x.dt == F16 && out.dt == F16 && (!b || b->dt == F16) && (!residual || residual->dt == F16),
+        "the fp16-compatible epilogue needs fp16 x, w, out and an fp16 (or no) bias and residual");
   REQ(out.defined() && out.dim() == 2 && out.size(0) == N && out.size(1) == Co &&
           (out.dt == F32 || out.dt == F16 || out.dt == BF16),
       "out must be [N,Co] f32/f16/bf16");

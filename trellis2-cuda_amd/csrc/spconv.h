@@ -48,12 +48,20 @@ struct SpConvCfg {
   int B1, BK, S;
 };
 SpConvCfg spconv_cfg(int N, int Ci, int Co);
+// The reference's tile choice for (N, Ci, Co) replayed from a FlexGEMM autotune cache file, section `device`
+// (src/spconv.cu:176-221); B1 = 128, BK = 64, S = 1 where the file has no entry.
+SpConvCfg spconv_cfg_autotune(const std::string& path, const std::string& device, i64 N, int Ci, int Co);
 
 // y = subm_conv3d(x, w, b): x fp16/bf16 [N,Ci], w same dtype [Co,27,Ci], b fp16/bf16/fp32 [Co] or null.
 // Returns [N,Co] in x's dtype; fp32 accumulation, bias added to the fp32 sum before the single rounding.
 Tensor subm_conv(const Tensor& x, const Tensor& w, const Tensor* b, SpConvCache& c);
 
 enum SpAct : int { ACT_NONE = 0, ACT_SILU = 1 };
+// Flag or'ed into a conv's act: fp16 rounding-compatible epilogue. Instead of one rounding of act(acc + b) + r, the
+// reference's sequence of fp16 roundings (src/spconv.cu:141-143, then act_ / add_, src/ops.cu:79-82,105-113):
+// y = f16(f16(acc) + b); y = f16(y / (1 + exp(-y))) for SiLU; y = f16(y + r). Needs fp16 x, w, out and an fp16 (or
+// no) bias and residual.
+constexpr int EPI_F16_COMPAT = 256;
 // Fused epilogue: out[i] = act(sum_v W_v x[nbr[i,v]] + b) [+ residual[i]], rounded once to out's dtype.
 // residual may be null; out must be a defined [N,Co] tensor of dtype F32, F16 or BF16.
 void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Tensor* residual, int act,

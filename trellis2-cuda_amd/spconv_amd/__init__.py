@@ -21,11 +21,12 @@ LIB_PATH = os.path.join(_PKG, "libspconv_amd.so")
 
 F32, F16, BF16 = 0, 1, 2
 ACT_NONE, ACT_SILU = 0, 1
+EPI_F16_COMPAT = 256  # or'ed into act: the reference's fp16 epilogue rounding sequence
 EMPTY = 0xFFFFFFFF
 
 # the C ABI's exported symbols (every declaration of include/spconv_amd.h)
 SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_cache_free", "spc_cache_info",
-           "spc_cache_valid", "spc_conv_cfg", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
+           "spc_cache_valid", "spc_conv_cfg", "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
            "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp",
            "spc_subdivide")
 
@@ -50,6 +51,8 @@ def load_library():
     L.spc_cache_info.argtypes = [P, ctypes.POINTER(I64), PP, PP, PP]
     L.spc_cache_valid.argtypes = [P, I, PP, PP, ctypes.POINTER(I64)]
     L.spc_conv_cfg.argtypes = [I64, I, I, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)]
+    L.spc_conv_cfg_autotune.argtypes = [ctypes.c_char_p, ctypes.c_char_p, I64, I, I, ctypes.POINTER(I),
+                                         ctypes.POINTER(I), ctypes.POINTER(I)]
     L.spc_subm_conv.argtypes = [P, P, P, I, I, I64, I, I, P, P]
     L.spc_subm_conv_fused.argtypes = [P, P, P, P, I, I, I, I, I, I64, I, I, P, P]
     L.spc_subm_conv_gathered.argtypes = [P, I64, P, I, P, P, P, I, I, I, I, I, I64, I, I, P, P]
@@ -172,6 +175,15 @@ def build_neighbors(coords, W: int = 4096, H: int = 4096, D: int = 4096) -> SpCo
 def spconv_cfg(N: int, Ci: int, Co: int):
     b1, bk, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     _check(load_library().spc_conv_cfg(N, Ci, Co, ctypes.byref(b1), ctypes.byref(bk), ctypes.byref(s)))
+    return b1.value, bk.value, s.value
+
+
+def spconv_cfg_autotune(path: str, device: str, N: int, Ci: int, Co: int):
+    """(B1, BK, S) the reference would pick from a FlexGEMM autotune cache file for device section `device`
+    (reference spconv_cfg, src/spconv.cu:176-221); (128, 64, 1) where the file has no entry. Host only."""
+    b1, bk, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _check(load_library().spc_conv_cfg_autotune(os.fsencode(path), device.encode(), N, Ci, Co, ctypes.byref(b1),
+                                                ctypes.byref(bk), ctypes.byref(s)))
     return b1.value, bk.value, s.value
 
 
