@@ -40,6 +40,25 @@ int spc_set_stream(void* hip_stream);
  * Replaces: build_neighbors (src/spconv.h:12, src/spconv.cu:38-54). */
 int spc_build_neighbors(const int32_t* coords, int64_t n, int W, int H, int D, spc_cache** out);
 
+/* As spc_build_neighbors, with flags: SPC_KEEP_HASH keeps the voxel hash in the cache (about 32-128 + 256 bytes
+ * per voxel) for spc_cache_lookup.
+ * Replaces: build_neighbors (src/spconv.cu:38-54) and the voxel hash builds of other consumers (k_vhash_insert,
+ * src/mesh.cu:8-13; the bake's hash, src/glb.cu:548-550), which can query this one instead. */
+enum { SPC_KEEP_HASH = 1 };
+int spc_build_neighbors_ex(const int32_t* coords, int64_t n, int W, int H, int D, int flags, spc_cache** out);
+
+/* rows[i] = the row of query[i] (int32 [m,4] = (b,x,y,z)) in the cache's voxels, or -1 when absent or outside the
+ * grid. Needs a cache built with SPC_KEEP_HASH (an empty cache answers -1).
+ * Replaces: vhash_find (src/mesh.cu:14-19) and the reference's per-offset probes (src/spconv.cu:22-36). */
+int spc_cache_lookup(const spc_cache* c, const int32_t* query, int64_t m, int32_t* rows);
+
+/* FlexiDualGrid quads from the cache's kernel map, no hash probes: for e = 3i + a, ok[e] = 1 and quad[e] = the rows
+ * of the 4 voxels at axis a's edge offsets when h[i, 3+a] > 0 (h f32 [n,7]) and all 4 exist, else ok[e] = 0 and
+ * quad[e] is left untouched. quad int32 [3n,4] (16-byte aligned), ok int32 [3n]. Matches the reference for a cache
+ * built over one batch with W = H = D = R.
+ * Replaces: k_fdg_quads and its hash (src/mesh.cu:7-19, 36-45, 54-62). */
+int spc_fdg_quads(const spc_cache* c, const float* h, int32_t* quad, int32_t* ok);
+
 /* Release a cache (its device buffers are freed in stream order). */
 int spc_cache_free(spc_cache* c);
 

@@ -100,3 +100,45 @@ def subdivide(coords: np.ndarray, logits_f16: np.ndarray):
     src = np.empty(m, np.int32)
     lib().orc_subdivide(_p(c), _p(lg), len(c), _p(oc), _p(src))
     return oc, src
+
+
+# FlexiDualGrid edge offsets per axis (reference c_edge_off, src/mesh.cu:20-24): the 4 voxels around voxel i's
+# edge along axis a, as (dx, dy, dz) added to (x, y, z).
+FDG_EDGE = (((0, 0, 0), (0, 0, 1), (0, 1, 1), (0, 1, 0)),
+            ((0, 0, 0), (1, 0, 0), (1, 0, 1), (0, 0, 1)),
+            ((0, 0, 0), (0, 1, 0), (1, 1, 0), (1, 0, 0)))
+
+
+def lookup(coords: np.ndarray, query: np.ndarray, W: int, H: int, D: int) -> np.ndarray:
+    """Row of each (b,x,y,z) query in coords, -1 if absent or outside [0,W)x[0,H)x[0,D) (a Python dict as the hash;
+    the probe of src/mesh.cu:14-19 with the batch kept in the key)."""
+    rows = {tuple(int(v) for v in c): i for i, c in enumerate(np.asarray(coords))}
+    out = np.full(len(query), -1, np.int32)
+    for j, (b, x, y, z) in enumerate(np.asarray(query).tolist()):
+        if b >= 0 and 0 <= x < W and 0 <= y < H and 0 <= z < D:
+            out[j] = rows.get((b, x, y, z), -1)
+    return out
+
+
+def fdg_quads(coords: np.ndarray, h: np.ndarray, R: int):
+    """(quad int32 [3n,4], ok int32 [3n]) of k_fdg_quads (src/mesh.cu:36-45) for one batch: e = 3i + a is kept when
+    h[i,3+a] > 0 and the 4 voxels at FDG_EDGE[a] exist inside [0,R)^3; quad rows of dropped edges are -1 here (the
+    reference leaves them unwritten). Pure Python: small cases only."""
+    c = np.asarray(coords)
+    rows = {(int(x), int(y), int(z)): i for i, (_, x, y, z) in enumerate(c.tolist())}
+    n = len(c)
+    quad = np.full((3 * n, 4), -1, np.int32)
+    ok = np.zeros(3 * n, np.int32)
+    for i in range(n):
+        _, x, y, z = (int(v) for v in c[i])
+        for a in range(3):
+            if not h[i, 3 + a] > 0:
+                continue
+            r = []
+            for dx, dy, dz in FDG_EDGE[a]:
+                p = (x + dx, y + dy, z + dz)
+                r.append(rows.get(p, -1) if all(0 <= v < R for v in p) else -1)
+            if min(r) >= 0:
+                ok[3 * i + a] = 1
+                quad[3 * i + a] = r
+    return quad, ok

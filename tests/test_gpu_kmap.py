@@ -121,3 +121,40 @@ def test_kmap_golden_fixture(gpu):
         lst, seg = cache.valid(B1)
         np.testing.assert_array_equal(lst.cpu().numpy(), g[f"list{B1}"])
         np.testing.assert_array_equal(seg.cpu().numpy(), g[f"seg{B1}"])
+
+
+@pytest.mark.parametrize("name", ["c1", "c2"])
+def test_lookup(gpu, name):
+    """Coordinate queries against the kept hash: every voxel finds its own row; shifted, other-batch, out-of-grid
+    and negative queries match a dictionary lookup."""
+    c = coords(name)
+    print(f"lookup case {name} n={len(c)}", flush=True)
+    R = 64 if name == "c2" else 32
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu), R, R, R, keep_hash=True)
+    rng = np.random.default_rng(3)
+    q = np.concatenate([c, c + np.array([0, 1, 0, 0], np.int32), c + np.array([1, 0, 0, 0], np.int32),
+                        rng.integers(-2, R + 2, size=(5000, 4)).astype(np.int32) * np.array([0, 1, 1, 1], np.int32)])
+    got = sp.lookup(cache, torch.from_numpy(q).to(gpu)).cpu().numpy()
+    np.testing.assert_array_equal(got[:len(c)], np.arange(len(c)))
+    np.testing.assert_array_equal(got, oracle.lookup(c, q, R, R, R))
+    with pytest.raises(RuntimeError):  # no hash kept
+        sp.lookup(sp.build_neighbors(torch.from_numpy(c).to(gpu), R, R, R), torch.from_numpy(q[:4]).to(gpu))
+    empty = sp.build_neighbors(torch.zeros((0, 4), dtype=torch.int32, device=gpu), R, R, R, keep_hash=True)
+    assert sp.lookup(empty, torch.from_numpy(q[:9]).to(gpu)).cpu().tolist() == [-1] * 9
+
+
+@pytest.mark.parametrize("name,R", [("c1", 32), ("c1", 20)])
+def test_fdg_quads(gpu, name, R):
+    """Quads from the kernel map equal the reference rule evaluated with a dictionary hash (ok flags everywhere,
+    quad rows where ok), including voxels cut by a tight grid bound."""
+    c = coords(name)
+    c = c[(c[:, 1:] < R).all(1)]
+    print(f"fdg case {name} R={R} n={len(c)}", flush=True)
+    h = np.random.default_rng(5).standard_normal((len(c), 7)).astype(np.float32)
+    cache = sp.build_neighbors(torch.from_numpy(np.ascontiguousarray(c)).to(gpu), R, R, R)
+    quad, ok = sp.fdg_quads(cache, torch.from_numpy(h).to(gpu))
+    oq, ook = oracle.fdg_quads(c, h, R)
+    ok = ok.cpu().numpy()
+    np.testing.assert_array_equal(ok, ook)
+    assert ok.sum() > 0
+    np.testing.assert_array_equal(quad.cpu().numpy()[ok == 1], oq[ook == 1])

@@ -212,3 +212,24 @@ def test_oracle_matches_golden_fixture():
     x, w, b, r = (bf16_bits_to_f32(g[k]) for k in ("x", "w", "b", "r"))
     y = oracle.conv(x, w, b, nbr, res=r, act=1)
     np.testing.assert_allclose(y, g["y_silu_res"], rtol=1e-5, atol=1e-5)
+
+
+def test_fdg_quads_known_answer():
+    """Four voxels filling the 2x2 square x = 0, y, z in {0,1}: only voxel (0,0,0)'s x-axis edge has all four
+    voxels ((0,0,0) (0,0,1) (0,1,1) (0,1,0), the x-axis edge offsets); a negative gate drops it."""
+    c = np.array([[0, 0, 1, 1], [0, 0, 0, 0], [0, 0, 1, 0], [0, 0, 0, 1]], np.int32)
+    h = np.ones((4, 7), np.float32)
+    quad, ok = oracle.fdg_quads(c, h, 8)
+    assert ok.tolist() == [0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0]
+    assert quad[3].tolist() == [1, 3, 0, 2]
+    h[1, 3] = -0.0
+    assert oracle.fdg_quads(c, h, 8)[1].sum() == 0
+    # the same square one voxel below the grid's top: the quad needs (0,1,1), which R = 1 excludes
+    assert oracle.fdg_quads(c, np.ones((4, 7), np.float32), 1)[1].sum() == 0
+
+
+def test_lookup_oracle():
+    c = np.array([[0, 1, 2, 3], [1, 1, 2, 3], [0, 4, 4, 4]], np.int32)
+    q = np.array([[0, 1, 2, 3], [1, 1, 2, 3], [2, 1, 2, 3], [0, 4, 4, 4], [0, 4, 4, 5], [-1, 1, 2, 3],
+                  [0, 8, 0, 0], [0, -1, 0, 0]], np.int32)
+    assert oracle.lookup(c, q, 8, 8, 8).tolist() == [0, 1, -1, 2, -1, -1, -1, -1]

@@ -51,6 +51,37 @@ SPC_API int spc_build_neighbors(const int32_t* coords, int64_t n, int W, int H, 
   });
 }
 
+SPC_API int spc_build_neighbors_ex(const int32_t* coords, int64_t n, int W, int H, int D, int flags,
+                                   spc_cache** out) {
+  return guarded([&] {
+    REQ(out, "out is null");
+    REQ(n >= 0 && (n == 0 || coords), "coords null or n < 0");
+    REQ((flags & ~SPC_KEEP_HASH) == 0, "unknown flags %d", flags);
+    auto h = std::make_unique<spc_cache>();
+    h->c = build_neighbors(borrow(coords, {n, 4}, I32), W, H, D, (flags & SPC_KEEP_HASH) != 0);
+    *out = h.release();
+  });
+}
+
+SPC_API int spc_cache_lookup(const spc_cache* c, const int32_t* query, int64_t m, int32_t* rows) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    REQ(m >= 0 && (m == 0 || (query && rows)), "null query/rows or m < 0");
+    Tensor tr = borrow(rows, {m}, I32);
+    lookup(c->c, borrow(query, {m, 4}, I32), tr);
+  });
+}
+
+SPC_API int spc_fdg_quads(const spc_cache* c, const float* h, int32_t* quad, int32_t* ok) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    const i64 n = c->c.N;
+    REQ(n == 0 || (h && quad && ok), "null h/quad/ok");
+    Tensor tq = borrow(quad, {3 * n, 4}, I32), to = borrow(ok, {3 * n}, I32);
+    fdg_quads(c->c, borrow(h, {n, 7}, F32), tq, to);
+  });
+}
+
 SPC_API int spc_cache_free(spc_cache* c) {
   return guarded([&] { delete c; });
 }

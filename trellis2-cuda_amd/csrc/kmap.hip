@@ -221,7 +221,7 @@ __global__ void k_c2s_emit(const uint4* __restrict__ lg, const int4* __restrict_
 }
 }  // namespace
 
-SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D) {
+SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep_hash) {
   REQ(coords.dt == I32 && coords.dim() == 2 && coords.size(1) == 4, "coords must be int32 [N,4]");
   REQ(W > 0 && H > 0 && D > 0, "grid %dx%dx%d", W, H, D);
   i64 n = coords.size(0);
@@ -251,7 +251,79 @@ SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D) {
                                                 c.gray.ptr<int32_t>(), bin.ptr<uint32_t>());
   CK(hipGetLastError());
   stable_argsort27(bin.ptr<uint32_t>(), n, c.sorted.ptr<int32_t>());
+  c.W = W;
+  c.H = H;
+  c.D = D;
+  if (keep_hash) {
+    c.htable = table;
+    c.hbricks = bricks;
+    c.hmask = (uint32_t)(cap - 1);
+  }
   return c;
+}
+
+namespace {
+__global__ void __launch_bounds__(256) k_lookup(const int4* __restrict__ q, i64 m, int W, int H, int D,
+                                                const ulonglong2* __restrict__ t, uint32_t mask,
+                                                const uint32_t* __restrict__ bricks, int32_t* __restrict__ out) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  const int4 c = q[i];
+  int32_t r = -1;
+  if (t && c.x >= 0 && c.y >= 0 && c.z >= 0 && c.w >= 0 && c.y < W && c.z < H && c.w < D) {  // t null: no voxels
+    const uint32_t id = brick_find(t, brick_key(c.x, c.y, c.z, c.w, (W + 3) >> 2, (H + 3) >> 2, (D + 3) >> 2), mask);
+    if (id != EMPTY) r = (int32_t)bricks[(i64)id * 64 + brick_local(c.y, c.z, c.w)];  // EMPTY reads as -1
+  }
+  out[i] = r;
+}
+
+// neighbour column of the offset (dx, dy, dz) in {-1, 0, 1}^3: v = (dx+1)*9 + (dy+1)*3 + (dz+1)
+__constant__ int8_t c_fdg_col[3][4] = {
+    {13, 14, 17, 16},  // axis x: (0,0,0) (0,0,1) (0,1,1) (0,1,0)
+    {13, 22, 23, 14},  // axis y: (0,0,0) (1,0,0) (1,0,1) (0,0,1)
+    {13, 16, 25, 22},  // axis z: (0,0,0) (0,1,0) (1,1,0) (1,0,0)
+};
+
+__global__ void __launch_bounds__(256) k_fdg_quads(const uint32_t* __restrict__ nbr, const float* __restrict__ h,
+                                                   i64 n, int4* __restrict__ quad, int32_t* __restrict__ ok) {
+  const i64 e = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= 3 * n) return;
+  const i64 i = e / 3;
+  const int a = (int)(e % 3);
+  bool g = h[i * 7 + 3 + a] > 0.f;
+  int r[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    r[k] = (int)nbr[i * 27 + c_fdg_col[a][k]];
+    g = g && r[k] >= 0;
+  }
+  ok[e] = g;
+  if (g) quad[e] = make_int4(r[0], r[1], r[2], r[3]);
+}
+}  // namespace
+
+void lookup(const SpConvCache& c, const Tensor& query, Tensor& rows) {
+  REQ(query.dt == I32 && query.dim() == 2 && query.size(1) == 4, "query must be int32 [M,4]");
+  REQ(rows.dt == I32 && rows.numel() == query.size(0), "rows must be int32 [M]");
+  const i64 m = query.size(0);
+  if (m == 0) return;
+  REQ(c.N == 0 || c.htable.defined(), "the cache was built without keep_hash");
+  k_lookup<<<cdiv(m, 256), 256, 0, stream()>>>(query.ptr<int4>(), m, c.W, c.H, c.D,
+                                               c.N ? (const ulonglong2*)c.htable.p : nullptr, c.hmask,
+                                               c.N ? c.hbricks.ptr<uint32_t>() : nullptr, rows.ptr<int32_t>());
+  CK(hipGetLastError());
+}
+
+void fdg_quads(const SpConvCache& c, const Tensor& h, Tensor& quad, Tensor& ok) {
+  const i64 n = c.N;
+  REQ(h.dt == F32 && h.dim() == 2 && h.size(0) == n && h.size(1) == 7, "h must be f32 [N,7]");
+  REQ(quad.dt == I32 && quad.numel() == 3 * n * 4 && ok.dt == I32 && ok.numel() == 3 * n,
+      "quad must be int32 [3N,4], ok int32 [3N]");
+  REQ((uintptr_t)quad.p % 16 == 0, "quad must be 16-byte aligned");
+  if (n == 0) return;
+  k_fdg_quads<<<cdiv(3 * n, 256), 256, 0, stream()>>>(c.nbr.ptr<uint32_t>(), h.ptr<float>(), n, quad.ptr<int4>(),
+                                                      ok.ptr<int32_t>());
+  CK(hipGetLastError());
 }
 
 const Tensor& SpConvCache::block_masks(int B1) {

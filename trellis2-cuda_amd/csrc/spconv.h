@@ -39,8 +39,27 @@ struct SpConvCache {
   // row_table(log2w).tbl with every non-EMPTY entry r replaced by row_map[r] >> shift, or EMPTY when that is not
   // below m (not memoized: row_map is the caller's). Used by the gathered conv.
   Tensor mapped_table(int log2w, const Tensor& row_map, int shift, i64 m);
+  // The brick hash, kept when built with keep_hash (for coordinate lookups by other consumers): slot table,
+  // brick records, slot mask and the grid bounds.
+  Tensor htable, hbricks;
+  uint32_t hmask = 0;
+  int W = 0, H = 0, D = 0;
 };
-SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D);  // coords int32 [N,4] (b,x,y,z)
+// coords int32 [N,4] (b,x,y,z); keep_hash keeps the brick hash in the cache (~32-128 B + 256 B per voxel) so that
+// lookup() can answer arbitrary coordinate queries.
+SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep_hash = false);
+
+// Row of each query coordinate (b,x,y,z) in the cache's voxel set, -1 when absent or outside [0,W)x[0,H)x[0,D)
+// (b < 0 included). The cache must have been built with keep_hash. Reference: the voxel hash probes of
+// mesh.cu:14-19 (vhash_find) and spconv.cu:22-36, answered by the brick hash.
+void lookup(const SpConvCache& c, const Tensor& query, Tensor& rows);
+
+// FlexiDualGrid quads from the kernel map, no hash probes (reference k_fdg_quads, src/mesh.cu:36-45): for voxel i
+// and axis a (e = 3i + a), if h[i,3+a] > 0 and the 4 voxels at the axis' edge offsets (all inside the 3x3x3
+// neighbourhood) exist, ok[e] = 1 and quad[e] = their rows, else ok[e] = 0 (quad[e] left untouched). h f32 [N,7],
+// quad int32 [3N,4], ok int32 [3N]. Equal to the reference when the cache was built with W = H = D = R over one
+// batch (the reference's mesh hash key ignores the batch).
+void fdg_quads(const SpConvCache& c, const Tensor& h, Tensor& quad, Tensor& ok);
 
 // Tile choice. The reference replays FlexGEMM's autotune table (src/spconv.cu:177-221); here the tile is fixed
 // per channel width (B1 = rows per tile and per schedule block, BK = channels per K stage, S = 1).

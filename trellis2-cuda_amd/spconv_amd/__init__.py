@@ -25,10 +25,10 @@ EPI_F16_COMPAT = 256  # or'ed into act: the reference's fp16 epilogue rounding s
 EMPTY = 0xFFFFFFFF
 
 # the C ABI's exported symbols (every declaration of include/spconv_amd.h)
-SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_cache_free", "spc_cache_info",
-           "spc_cache_valid", "spc_conv_cfg", "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
-           "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp",
-           "spc_subdivide")
+SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build_neighbors_ex", "spc_cache_lookup",
+           "spc_fdg_quads", "spc_cache_free", "spc_cache_info", "spc_cache_valid", "spc_conv_cfg",
+           "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
+           "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subdivide")
 
 _lib = None
 
@@ -47,6 +47,9 @@ def load_library():
     L.spc_last_error.argtypes = []
     L.spc_set_stream.argtypes = [P]
     L.spc_build_neighbors.argtypes = [P, I64, I, I, I, PP]
+    L.spc_build_neighbors_ex.argtypes = [P, I64, I, I, I, I, PP]
+    L.spc_cache_lookup.argtypes = [P, P, I64, P]
+    L.spc_fdg_quads.argtypes = [P, P, P, P]
     L.spc_cache_free.argtypes = [P]
     L.spc_cache_info.argtypes = [P, ctypes.POINTER(I64), PP, PP, PP]
     L.spc_cache_valid.argtypes = [P, I, PP, PP, ctypes.POINTER(I64)]
@@ -163,13 +166,39 @@ def _memcpy_d2d(dst: int, src: int, nbytes: int) -> None:
         raise RuntimeError(f"hipMemcpy failed ({rc})")
 
 
-def build_neighbors(coords, W: int = 4096, H: int = 4096, D: int = 4096) -> SpConvCache:
+def build_neighbors(coords, W: int = 4096, H: int = 4096, D: int = 4096, keep_hash: bool = False) -> SpConvCache:
+    """Kernel map of coords (int32 [N,4] = (b,x,y,z)) in a W x H x D grid (reference build_neighbors,
+    src/spconv.cu:38-54). keep_hash keeps the voxel hash for lookup()."""
     torch = _torch()
     if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
         raise ValueError("coords must be int32 [N,4]")
     h = ctypes.c_void_p()
-    _check(load_library().spc_build_neighbors(_ptr(coords), coords.shape[0], W, H, D, ctypes.byref(h)))
+    _check(load_library().spc_build_neighbors_ex(_ptr(coords), coords.shape[0], W, H, D, 1 if keep_hash else 0,
+                                                 ctypes.byref(h)))
     return SpConvCache(h, coords.shape[0], coords.device)
+
+
+def lookup(cache: SpConvCache, query):
+    """Row of each (b,x,y,z) query (int32 [M,4]) in the cache's voxels, -1 when absent or outside the grid; the cache
+    must be built with keep_hash (reference vhash_find, src/mesh.cu:14-19)."""
+    torch = _torch()
+    if query.dtype != torch.int32 or query.dim() != 2 or query.shape[1] != 4:
+        raise ValueError("query must be int32 [M,4]")
+    rows = torch.empty(query.shape[0], dtype=torch.int32, device=query.device)
+    _check(load_library().spc_cache_lookup(cache._h, _ptr(query), query.shape[0], _ptr(rows)))
+    return rows
+
+
+def fdg_quads(cache: SpConvCache, h):
+    """FlexiDualGrid quads from the kernel map (reference k_fdg_quads, src/mesh.cu:36-45): returns (quad int32
+    [3N,4], ok int32 [3N]); quad rows of edges with ok = 0 are unspecified."""
+    torch = _torch()
+    if h.dtype != torch.float32 or h.dim() != 2 or h.shape != (cache.N, 7):
+        raise ValueError(f"h must be float32 [{cache.N},7]")
+    quad = torch.full((3 * cache.N, 4), -1, dtype=torch.int32, device=h.device)
+    ok = torch.empty(3 * cache.N, dtype=torch.int32, device=h.device)
+    _check(load_library().spc_fdg_quads(cache._h, _ptr(h), _ptr(quad), _ptr(ok)))
+    return quad, ok
 
 
 def spconv_cfg(N: int, Ci: int, Co: int):
