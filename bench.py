@@ -46,6 +46,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured copy / GEMM ceilings")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the upsample-block and ConvNeXt-tail extras (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy (the counter calibration used by bench_profile.py)")
     args = ap.parse_args()
@@ -183,7 +185,7 @@ def main():
                     "frac_of_measured": round((tflops / gemm_tf) if wide else (gbs / copy_gbs), 4)}
 
     e2e = None
-    if cfg.subdivide:
+    if cfg.subdivide and not args.no_extras:
         # cascade upsample block end to end: subdivide -> rehash + kernel map -> conv of the children, which read
         # their parents' rows through the c2s map (no gathered child features are written)
         lgt = torch.from_numpy(lg.view(np.int16)).to(dev).view(torch.float16)
@@ -235,7 +237,7 @@ def main():
     # the decoder's ConvNeXt tail on this layer's output rows (LayerNorm + affine -> Linear 4C + SiLU -> Linear C ->
     # + x, reference src/sdec.cu:60-66), fused, against torch's unfused sequence on the same tensors
     tail = None
-    if co in (64, 128, 256):
+    if co in (64, 128, 256) and not args.no_extras:
         hx = torch.randn((n, co), generator=g, device=dev).to(torch.bfloat16)
         xx = torch.randn((n, co), generator=g, device=dev).to(torch.bfloat16)
         gm, bt = torch.ones(co, device=dev), torch.zeros(co, device=dev)

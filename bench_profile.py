@@ -61,10 +61,13 @@ def main():
     os.makedirs(out, exist_ok=True)
     py = sys.executable
     bench = [py, os.path.join(ROOT, "bench.py"), "--config", args.config, "--steps", str(args.steps), "--warmup", "2",
-             "--no-cpu", "--no-peaks"]
+             "--no-cpu", "--no-peaks", "--no-extras"]
     copy = [py, os.path.join(ROOT, "bench.py"), "--calibrate-copy"]
     rp = ["rocprofv3", "--output-format", "csv", "-o", "run"]
 
+    # the same command without the profiler: its event-timed step, to set beside the profiled kernel average
+    run(bench, 120, f"{out}/plain.log")
+    plain = json.loads([l for l in open(f"{out}/plain.log") if l.startswith("{")][-1])
     run(rp + ["--kernel-trace", "--stats", "-d", f"{out}/trace", "--"] + bench, 300, f"{out}/trace.log")
     stats = csv_rows(f"{out}/trace", "kernel_stats.csv")
     stats.sort(key=lambda r: -float(r["TotalDurationNs"]))
@@ -86,7 +89,7 @@ def main():
            "fetch_KiB": figs["FETCH_SIZE"][0], "write_KiB": figs["WRITE_SIZE"][0],
            "copy_fetch_KiB": figs["copy_FETCH_SIZE"][0], "copy_write_KiB": figs["copy_WRITE_SIZE"][0],
            "copy_bytes": COPY_BYTES, "fetch_factor": fetch_factor, "write_factor": write_factor,
-           "traffic_bytes": fetch_b + write_b}
+           "traffic_bytes": fetch_b + write_b, "plain_ms_per_step": plain["ms_per_step"]}
     prof = args.profiles_dir
     os.makedirs(prof, exist_ok=True)
     with open(os.path.join(prof, f"traffic_{args.config}.json"), "w") as f:
@@ -106,7 +109,10 @@ def main():
     for r in stats[:8]:
         md.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                   f"{float(r['TotalDurationNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
-    md += ["", "## HBM traffic of the dominant kernel (per dispatch)", "",
+    md += ["", f"Without the profiler the same command times a step (weight repack + this kernel, HIP events on the "
+           f"library's stream) at {plain['ms_per_step'] * 1e3:.1f} us; the profiled average above is "
+           f"{float(top['AverageNs']) / 1e3:.1f} us.", "",
+           "## HBM traffic of the dominant kernel (per dispatch)", "",
            f"- FETCH_SIZE {figs['FETCH_SIZE'][0]:.0f} KiB ({figs['FETCH_SIZE'][1]} dispatches), "
            f"WRITE_SIZE {figs['WRITE_SIZE'][0]:.0f} KiB",
            f"- calibration: a {COPY_BYTES >> 20} MiB device copy reads FETCH_SIZE {figs['copy_FETCH_SIZE'][0]:.0f} KiB "

@@ -214,11 +214,14 @@ def test_gathered_conv(gpu, ci, co):
         compare(y1, ref, "f32", f"gathered ci={ci} co={co} act={act}")
 
 
-@pytest.mark.parametrize("ci,co", [(64, 64), (64, 128), (256, 256), (128, 192)])
+@pytest.mark.parametrize("ci,co", [(128, 192), (96, 192), (64, 320), (64, 64), (256, 256)])
 def test_f16_compat_epilogue(gpu, ci, co):
-    """EPI_F16_COMPAT reproduces the reference's rounding sequence on the kernel's own fp32 sums: f16(f16(acc) + b),
-    then SiLU rounded to f16, then the residual add rounded to f16. Checked against that sequence applied on the host
-    to the same kernel's fp32 output without bias: bit-exact without SiLU; with SiLU the host exp may differ from
+    """EPI_F16_COMPAT reproduces the reference's rounding sequence on the kernel's fp32 sums: f16(f16(acc) + b),
+    then SiLU rounded to f16, then the residual add rounded to f16. It always runs in the generic kernel; for widths
+    the generic kernel also serves without the flag (Co not a multiple of 128, Co != 64) the sequence is checked
+    against the host applying it to that kernel's fp32 output without bias: bit-exact without SiLU; for the tuned
+    widths (64 -> 64, 256 -> 256) the sums come from another kernel, so up to 1e-3 of the elements may differ by
+    one fp16 ulp of the rounded sum plus one of the result. With SiLU the host exp may differ from
     the device's in the last fp32 bit, so at most 1e-3 of the elements may differ, by one fp16 ulp (plus, after a residual
     add, one ulp of the SiLU value that differed)."""
     c = shell(7.0)
@@ -235,7 +238,9 @@ def test_f16_compat_epilogue(gpu, ci, co):
     for act in (0, 1):
         for res in (None, rs):
             y = sp.subm_conv_fused(xs, ws, bs, cache, residual=res, act=act | sp.EPI_F16_COMPAT).cpu()
-            e = (acc.half().float() + tb.float()).half().float()
+            a16 = acc.half().float()  # the first rounding: a one-ulp difference there survives the bias add
+            e = (a16 + tb.float()).half().float()
+            y1 = e.clone()  # after the bias add
             if act:
                 e = (e.double() / (1 + torch.exp(-e.double()))).float().half().float()
             s = e.clone()  # the SiLU value: a one-ulp difference there survives the residual add
@@ -244,7 +249,8 @@ def test_f16_compat_epilogue(gpu, ci, co):
             e = e.half()
             what = f"ci={ci} co={co} act={act} res={res is not None}"
             assert y.dtype == torch.float16, what
-            if not act:
+            generic = co % 128 != 0 and co != 64
+            if not act and generic:
                 assert torch.equal(y, e), what
             else:
                 d = (y.float() - e.float()).abs()
@@ -252,6 +258,8 @@ def test_f16_compat_epilogue(gpu, ci, co):
                 what += f": {int(bad.sum())} of {bad.numel()} differ, max {float(d.max()):.3g}"
                 assert bad.float().mean() <= 1e-3, what
                 tol = ulp(e.float()[bad].numpy(), "f16") + (ulp(s[bad].numpy(), "f16") if res is not None else 0)
+                if not generic:  # each earlier rounding may differ by one ulp, carried through SiLU's slope (< 1.1)
+                    tol = tol + 1.1 * (ulp(a16[bad].numpy(), "f16") + ulp(y1[bad].numpy(), "f16"))
                 assert torch.all(d[bad] <= torch.from_numpy(tol)), what
     with pytest.raises(RuntimeError):  # bf16 is not a compat dtype
         sp.subm_conv_fused(xs.bfloat16(), ws.bfloat16(), None, cache, act=sp.EPI_F16_COMPAT)

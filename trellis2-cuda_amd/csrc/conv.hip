@@ -282,7 +282,7 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 struct Epi {
   __amdgpu_buffer_rsrc_t out, res;
   int out_dt, res_dt;  // res_dt < 0: no residual
-  bool silu, compat;   // compat: the fp16 rounding sequence (EPI_F16_COMPAT)
+  bool silu;
 };
 __device__ __forceinline__ Epi make_epi(const ConvArgs& a) {
   Epi e;
@@ -290,8 +290,7 @@ __device__ __forceinline__ Epi make_epi(const ConvArgs& a) {
   e.res = make_rsrc(a.res, a.res_bytes);
   e.out_dt = a.out_dt;
   e.res_dt = a.res ? a.res_dt : -1;
-  e.silu = (a.act & ~EPI_F16_COMPAT) == ACT_SILU;
-  e.compat = (a.act & EPI_F16_COMPAT) != 0;
+  e.silu = a.act == ACT_SILU;  // the tiled kernels never see EPI_F16_COMPAT (dispatch sends it to k_conv)
   return e;
 }
 
@@ -310,18 +309,6 @@ __device__ __forceinline__ void load_res8(const Epi& e, uint32_t o, bool ok, u32
 // out[o .. o+8) = act(v + bias) [+ residual r], one rounding to the output dtype
 __device__ __forceinline__ void store_row8(const Epi& e, uint32_t o, bool ok, float (&v)[8], const float (&bias8)[8],
                                            const u32x4 (&r)[2]) {
-  if (e.compat) {  // fp16 x/out/bias/residual (checked on the host)
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-      v[q] = f16r(f16r(v[q]) + bias8[q]);
-      if (e.silu) v[q] = f16r(silu_ieee(v[q]));
-      if (e.res_dt == F16) v[q] = v[q] + f16_to_f32((uint16_t)(r[0][q >> 1] >> ((q & 1) * 16)));
-    }
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{pack2<false>(v[0], v[1]), pack2<false>(v[2], v[3]),
-                                                 pack2<false>(v[4], v[5]), pack2<false>(v[6], v[7])},
-                                           e.out, ok ? o * 2u : kOutOfRange, 0, 0);
-    return;
-  }
 #pragma unroll
   for (int q = 0; q < 8; q++) v[q] += bias8[q];
   if (e.silu) {
@@ -1153,7 +1140,10 @@ void launch(ConvArgs a) {
 
 template <bool F16>
 void dispatch(const SpConvCfg& cfg, ConvArgs a) {
-  if (a.Co == 64 && a.Ci <= 128) {
+  // The fp16-compatible epilogue runs in the generic kernel only: its longer rounding sequence (IEEE quotient,
+  // accurate exp) would cost the tuned kernels registers in their epilogues.
+  const bool compat = a.act & EPI_F16_COMPAT;
+  if (!compat && a.Co == 64 && a.Ci <= 128) {
     switch (a.Ci / 32) {
       case 1: return launch_narrow<F16, 1, 4>(a);
       case 2: return launch_narrow<F16, 2, 4>(a);
@@ -1162,8 +1152,8 @@ void dispatch(const SpConvCfg& cfg, ConvArgs a) {
     }
   }
   // Fixed tiles per channel width (no autotune): BM = 128 sorted rows per tile.
-  if (cfg.BK == 64 && a.Co % 256 == 0) return launch_wide_dma<F16>(a);
-  if (cfg.BK == 64 && a.Co % 128 == 0) return launch_wide<F16, 2, 128>(a);
+  if (!compat && cfg.BK == 64 && a.Co % 256 == 0) return launch_wide_dma<F16>(a);
+  if (!compat && cfg.BK == 64 && a.Co % 128 == 0) return launch_wide<F16, 2, 128>(a);
   if (a.Co % 128 == 0) {
     if (cfg.BK == 64) launch<F16, 128, 128, 2, 2, 64>(a);
     else launch<F16, 128, 128, 2, 2, 32>(a);
@@ -1182,8 +1172,8 @@ SpConvCfg spconv_cfg(int N, int Ci, int Co) {
 
 // The kernels that read their tiles' neighbour rows from the tile-order table (narrow, 256-channel wide) can read
 // them through a row map instead; the others get the gathered rows materialized.
-bool reads_row_table(const SpConvCfg& cfg, int Ci, int Co) {
-  return (Co == 64 && Ci <= 128) || (cfg.BK == 64 && Co % 256 == 0);
+bool reads_row_table(const SpConvCfg& cfg, int Ci, int Co, int act) {
+  return !(act & EPI_F16_COMPAT) && ((Co == 64 && Ci <= 128) || (cfg.BK == 64 && Co % 256 == 0));
 }
 
 __global__ void k_gather_rows(const u32x4* __restrict__ x, i64 m, int units, const int32_t* __restrict__ row_map,
@@ -1263,9 +1253,10 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   a.Co = Co;
   a.act = act;
   Tensor wpack, mtbl;
-  REQ(!row_map || reads_row_table(cfg, Ci, Co), "row map with a kernel that reads nbr directly");
+  REQ(!row_map || reads_row_table(cfg, Ci, Co, act), "row map with a kernel that reads nbr directly");
+  const bool compat = act & EPI_F16_COMPAT;
   const i64 chunks = (i64)Co * 27 * Ci / 8;
-  if (Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, rows in spatial order
+  if (!compat && Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, spatial row order
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
@@ -1275,7 +1266,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
     a.gs = rt.gs.ptr<int32_t>();
     a.tbl_bytes = (uint32_t)rt.tbl.bytes();
-  } else if (cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
+  } else if (!compat && cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
@@ -1304,7 +1295,7 @@ void subm_conv_gathered(const Tensor& x_src, const Tensor& row_map, int shift, c
   REQ(shift >= 0 && shift < 31, "shift=%d", shift);
   const int Ci = (int)x_src.size(1), Co = (int)w.size(0);
   REQ(Ci > 0 && Ci % 32 == 0 && Ci <= kMaxCi, "Ci=%d must be a multiple of 32 (at most %d)", Ci, kMaxCi);
-  if (c.N == 0 || reads_row_table(spconv_cfg(c.N, Ci, Co), Ci, Co)) {
+  if (c.N == 0 || reads_row_table(spconv_cfg(c.N, Ci, Co), Ci, Co, act)) {
     conv_impl(x_src, &row_map, shift, w, b, residual, act, c, out);
     return;
   }
