@@ -113,10 +113,11 @@ def main():
     # MFMA padding: the kernels skip an offset per group of rows (32 sorted rows in the wide kernel, 16 rows of the
     # 65536-row windowed order in the narrow one), so executed pairs = sum over groups of rows x |OR of masks|
     narrow = co == 64 and ci <= 128
+    halo = co == 64 and ci == 64 and not os.environ.get("SPCONV_NO_HALO")  # 256-row windows (halo kernel)
     gsz = 16 if narrow else 32
     order = srt.cpu().numpy().astype(np.int64)
     if narrow:
-        order = order[np.argsort(order >> 16, kind="stable")]
+        order = order[np.argsort(order >> (8 if halo else 16), kind="stable")]
     gm = gray.cpu().numpy().astype(np.int64)[order]
     ng = (n + gsz - 1) // gsz
     pad = np.zeros(ng * gsz, np.int64)
@@ -128,6 +129,12 @@ def main():
     def step():
         sp.subm_conv_fused(x, w, b, cache, residual=res, act=act, out=y)
 
+    # the first call also builds the cache's memoized schedules for this layer shape (tile tables, halo lists)
+    torch.cuda.synchronize()
+    t_first = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    first_ms = (time.perf_counter() - t_first) * 1e3
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -297,7 +304,8 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "extras": {"mvox_per_s": round(mvox, 2), "compulsory_GBps": round(gbs, 1),
-                   "kmap_build_ms": round(float(np.median(map_ms)), 4), "coord_gen_s": round(gen_s, 2),
+                   "kmap_build_ms": round(float(np.median(map_ms)), 4), "first_call_ms": round(first_ms, 3),
+                   "coord_gen_s": round(gen_s, 2),
                    "executed_over_active_pairs": round(executed_pairs / max(P, 1), 4), "skip_group_rows": gsz, "wall_s": round(wall, 3),
                    "upsample_block_e2e": e2e, "convnext_tail": tail, "measured_peaks": measured},
     }

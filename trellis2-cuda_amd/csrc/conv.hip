@@ -104,6 +104,10 @@ struct ConvArgs {
   const int32_t* gs;    // neighbour masks in tile order
   const int32_t* gray;
   const uint32_t* code;
+  const int32_t* hrows;    // halo schedule (SpConvCache::halo_table), for k_conv_halo
+  const int32_t* hcount;
+  const uint16_t* hidx;
+  const uint32_t* hgm;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
   uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes, out_bytes, tbl_bytes;
@@ -866,6 +870,193 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   }
 }
 
+// Halo kernel (Ci = Co = 64): a workgroup owns a 256-row window of the input (spatial) order, its rows gray-sorted
+// (SpConvCache::halo_table: tight 16-row neighbour masks, 1.22x the active pairs on C4 against 1.81x unsorted).
+// Before its K
+// loop it copies, by DMA, every distinct neighbour row the tile reads (the tile's halo, ~1.4 rows per output row on
+// shells instead of ~7.7 gathers) into LDS, plus the tile's (row, offset) -> halo index table; the K loop then
+// reads its A operands from LDS with no barriers (each wavefront walks its own offsets) and its weights straight
+// from L2 into registers, one offset ahead. Halo rows are stored with their 16-byte chunks XOR-swizzled by the
+// halo index (conflict-light operand reads); index kHaloMax is a zero row that EMPTY neighbours point at. Two
+// workgroups per CU (LDS 80 KB each): one copies its halo while the other computes. Outputs and residuals are
+// whole rows of the window, permuted inside it.
+template <bool F16, int G, int T>
+__global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
+  // wavefront (wr, wc) owns rows wr*16G .. +16G (G groups of 16) x output tiles wc*T .. +T (16 channels each)
+  constexpr int B = SpConvCache::kHaloRows, UM = SpConvCache::kHaloMax, CO = 64, S = 2;
+  constexpr int WC = 4 / T;  // wavefronts across the channels
+  static_assert(4 * 16 * G * T == B * 4, "4 wavefronts cover 256 rows x 4 channel tiles");
+  constexpr int IDXU = 27 * B * 2 / 16;      // 16-byte units of the index table
+  constexpr int IDXP = (IDXU + 63) / 64 * 64;  // padded to whole wavefront DMA instructions (the tail reads zeros)
+  static_assert(B == 256, "tile shape");
+  __shared__ __attribute__((aligned(16))) u32x4 halo[(UM + 1) * 8];
+  __shared__ __attribute__((aligned(16))) u32x4 idxL[IDXP];
+  __shared__ uint32_t gmL[B / 16];
+  const int g = blockIdx.x, per = a.grid / 8;
+  const int tile = (g % 8) * per + g / 8;
+  if (tile >= a.tiles_m) return;
+  const int row0 = tile * B;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
+  const int wr = wv / WC, wc = wv % WC;
+  const int N = a.N;
+  const int U = __builtin_amdgcn_readfirstlane(a.hcount[tile]);
+
+  // prologue: index table and halo rows by DMA, the zero row and the group masks by plain stores
+  {
+    const __amdgpu_buffer_rsrc_t ri = make_rsrc(a.hidx + (size_t)tile * 27 * B, 27 * B * 2);
+#pragma unroll
+    for (int k = 0; k < (IDXP + 255) / 256; k++) {
+      const int u = k * 256 + tid;
+      if (k * 256 + wv * 64 < IDXP)  // wave-uniform: DMA destinations are per wavefront instruction
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ri, (__attribute__((address_space(3))) void*)&idxL[k * 256 + wv * 64],
+                                                 16, (uint32_t)u * 16u, 0, 0, 0);
+    }
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
+    const int32_t* hr = a.hrows + (size_t)tile * UM;
+    const int nins = (U * 8 + 63) / 64;  // wavefront instructions of 64 x 16 bytes (8 halo rows each)
+    for (int j = wv; j < nins; j += 4) {
+      const int unit = j * 64 + lane, u = unit >> 3, c = unit & 7;
+      const int h = u < U ? hr[u] : -1;
+      const uint32_t off = h >= 0 ? (uint32_t)h * 128u + (uint32_t)((c ^ (u & 7)) * 16) : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)&halo[j * 64], 16, off, 0,
+                                               0, 0);
+    }
+    if (tid < 8) halo[UM * 8 + tid] = u32x4{0, 0, 0, 0};
+    if (tid < B / 16) gmL[tid] = a.hgm[(size_t)tile * (B / 16) + tid];
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  // epilogue layout (16-byte row segments, LPR lanes per row) and the output rows, fetched now for later
+  constexpr int ES = 16 * T + 4, LPR = 2 * T, RPP = 64 / LPR, NP = 16 / RPP;
+  const int c8 = wc * 16 * T + (lane % LPR) * 8;
+  int orow[G][NP];
+#pragma unroll
+  for (int i = 0; i < G; i++)
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const int pos = row0 + wr * 16 * G + i * 16 + p * RPP + lane / LPR;
+      orow[i][p] = pos < N ? a.order[pos] : 0;
+    }
+  uint32_t gms[G], wmask = 0;
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    gms[i] = __builtin_amdgcn_readfirstlane(gmL[wr * G + i]);
+    wmask |= gms[i];
+  }
+  f32x4v acc[G][T];
+#pragma unroll
+  for (int i = 0; i < G; i++)
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[i][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.w_bytes);
+  const uint16_t* idx16 = (const uint16_t*)idxL;
+  auto wload = [&](int v, u32x4 (&w)[T][S]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int m = 0; m < S; m++)
+        w[t][m] = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(((v * 4 + wc * T + t) * S + m) * 64 + lane) * 16u,
+                                                        0, 0);
+  };
+  // A operands of offset v for every group (idle groups read the zero row: LDS reads are cheap, and reading them
+  // unconditionally lets the reads of the next offset be issued before this offset's MFMAs)
+  auto aload = [&](int v, u32x4 (&av)[G][S]) __attribute__((always_inline)) {
+    int u[G];
+#pragma unroll
+    for (int i = 0; i < G; i++) u[i] = idx16[v * B + wr * 16 * G + i * 16 + r16];
+#pragma unroll
+    for (int i = 0; i < G; i++)
+#pragma unroll
+      for (int m = 0; m < S; m++) av[i][m] = halo[u[i] * 8 + ((2 * q4 + m) ^ (u[i] & 7))];
+  };
+  auto compute = [&](int v, const u32x4 (&w)[T][S], const u32x4 (&av)[G][S]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      if ((gms[i] >> v) & 1u) {
+#pragma unroll
+        for (int m = 0; m < S; m++)
+#pragma unroll
+          for (int t = 0; t < T; t++) acc[i][t] = mfma16<F16>(av[i][m], w[t][m], acc[i][t]);
+      }
+    }
+  };
+  // offsets of this wavefront in ascending order; the weights (from L2) and A operands (from LDS) of the next one
+  // are requested while this one computes. The weight load is unconditional -- the last offset reloads itself --
+  // so the compiler's wait counts stay exact.
+  if (wmask) {
+    uint32_t m = wmask;
+    int v = __builtin_ctz(m);
+    m &= m - 1;
+    u32x4 wa[T][S], wb[T][S], aa[G][S], ab[G][S];
+    wload(v, wa);
+    aload(v, aa);
+    for (;;) {
+      int vn = m ? __builtin_ctz(m) : v;
+      wload(vn, wb);
+      aload(vn, ab);
+      compute(v, wa, aa);
+      if (!m) break;
+      m &= m - 1;
+      v = vn;
+      vn = m ? __builtin_ctz(m) : v;
+      wload(vn, wa);
+      aload(vn, aa);
+      compute(v, wb, ab);
+      if (!m) break;
+      m &= m - 1;
+      v = vn;
+    }
+  }
+
+  // epilogue: per 16-row group through a per-wavefront [16][CO+4] fp32 area in the (now idle) halo buffer; the
+  // output rows (orow, read before the K loop) and every group's residual are requested up front
+  __syncthreads();  // every wavefront is done reading the halo
+  float* ew = (float*)halo + wv * 16 * ES;
+  float bias8[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[c8 + q] : 0.f;
+  const Epi e = make_epi(a);
+  u32x4 resv[G][NP][2];
+#pragma unroll
+  for (int i = 0; i < G; i++)
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+      load_res8(e, (uint32_t)orow[i][p] * CO + c8, row0 + wr * 16 * G + i * 16 + p * RPP + lane / LPR < N, resv[i][p]);
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) ew[(q4 * 4 + q) * ES + t * 16 + r16] = acc[i][t][q];
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const int rr = p * RPP + lane / LPR;
+      const int pos = row0 + wr * 16 * G + i * 16 + rr;
+      const int lc = (lane % LPR) * 8;  // column within this wavefront's channels
+      float v8[8];
+      *(f32x4*)&v8[0] = *(const f32x4*)&ew[rr * ES + lc];
+      *(f32x4*)&v8[4] = *(const f32x4*)&ew[rr * ES + lc + 4];
+      store_row8(e, (uint32_t)orow[i][p] * CO + c8, pos < N, v8, bias8, resv[i][p]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  }
+}
+
+template <bool F16>
+void launch_halo(ConvArgs a) {
+  a.tiles_m = cdiv(a.N, SpConvCache::kHaloRows);
+  a.tiles_n = 1;
+  a.grid = (a.tiles_m + 7) / 8 * 8;
+#ifndef HALO_GT
+#define HALO_GT 4, 4
+#endif
+  k_conv_halo<F16, HALO_GT><<<a.grid, 256, 0, stream()>>>(a);
+}
+
 template <bool F16, int S, int T>
 void launch_narrow(ConvArgs a) {
   constexpr int G = S <= 2 ? 4 : 2;  // 16-row groups per wavefront: keeps two wavefronts per SIMD at Ci = 128
@@ -1143,6 +1334,7 @@ void dispatch(const SpConvCfg& cfg, ConvArgs a) {
   // The fp16-compatible epilogue runs in the generic kernel only: its longer rounding sequence (IEEE quotient,
   // accurate exp) would cost the tuned kernels registers in their epilogues.
   const bool compat = a.act & EPI_F16_COMPAT;
+  if (a.hrows) return launch_halo<F16>(a);
   if (!compat && a.Co == 64 && a.Ci <= 128) {
     switch (a.Ci / 32) {
       case 1: return launch_narrow<F16, 1, 4>(a);
@@ -1183,6 +1375,15 @@ __global__ void k_gather_rows(const u32x4* __restrict__ x, i64 m, int units, con
   const i64 i = q / units;
   const uint32_t r = (uint32_t)row_map[i] >> shift;
   out[q] = r < (uint64_t)m ? x[(i64)r * units + (q - i * units)] : u32x4{0, 0, 0, 0};
+}
+
+// The halo kernel serves Ci = Co = 64 unless SPCONV_NO_HALO is set (then the gathering narrow kernel does).
+bool halo_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("SPCONV_NO_HALO");
+    return !(e && e[0] && e[0] != '0');
+  }();
+  return on;
 }
 
 // x: the conv input [N,Ci], or with row_map the source rows [M,Ci] read through row_map >> shift
@@ -1256,7 +1457,21 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   REQ(!row_map || reads_row_table(cfg, Ci, Co, act), "row map with a kernel that reads nbr directly");
   const bool compat = act & EPI_F16_COMPAT;
   const i64 chunks = (i64)Co * 27 * Ci / 8;
-  if (!compat && Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, spatial row order
+  const SpConvCache::HaloTable* ht = nullptr;
+  if (!compat && !row_map && Co == 64 && Ci == 64 && halo_enabled()) {
+    ht = &c.halo_table();
+    if (!ht->ok) ht = nullptr;
+  }
+  if (ht) {  // halo kernel: narrow weight order, the tile's distinct neighbour rows copied to LDS once
+    wpack = empty({(i64)Co * 27 * Ci}, x.dt);
+    k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
+    a.w = wpack.ptr<uint16_t>();
+    a.hrows = ht->rows.ptr<int32_t>();
+    a.hcount = ht->count.ptr<int32_t>();
+    a.hidx = (const uint16_t*)ht->idx.p;
+    a.hgm = ht->gm.ptr<uint32_t>();
+    a.order = ht->order.ptr<int32_t>();
+  } else if (!compat && Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, spatial row order
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();

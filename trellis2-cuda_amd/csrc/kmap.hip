@@ -473,3 +473,116 @@ Subdivision subdivide(const Tensor& coords, const Tensor& logits) {
   }
   return o;
 }
+
+// ------------------------------------------------------------------------------------------ halo schedule
+namespace {
+constexpr int kHaloSlots = 1024;  // LDS hash slots per tile (>= 2 * kHaloMax)
+
+__global__ void k_fill_i32(int32_t* __restrict__ p, i64 n, int32_t v) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// One workgroup per tile of kHaloRows input-order rows, one thread per row. The tile's neighbour rows go into an
+// LDS open-addressed set (linear probing, at most kHaloSlots probes: a tile with more distinct rows is flagged);
+// occupied slots are then numbered by a workgroup prefix count, which gives the halo list and every (row, offset)
+// its index in it. The list order follows the slots (not deterministic under concurrent inserts) -- only where a
+// row sits in the conv's LDS copy depends on it, never a sum.
+__global__ void __launch_bounds__(256) k_halo_build(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ order,
+                                                    i64 n, int32_t* __restrict__ rows,
+                                                    int32_t* __restrict__ count, uint16_t* __restrict__ idx,
+                                                    uint32_t* __restrict__ gm, int32_t* __restrict__ overflow) {
+  constexpr int B = SpConvCache::kHaloRows, UM = SpConvCache::kHaloMax;
+  static_assert(B == 256, "one thread per row");
+  __shared__ uint32_t keys[kHaloSlots];
+  __shared__ int pos[kHaloSlots];
+  __shared__ int wsum[4];
+  __shared__ int bad;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const i64 t = blockIdx.x, p = t * B + tid;  // position in the tile order; its row is order[p]
+  const i64 r = p < n ? order[p] : n;
+  for (int i = tid; i < kHaloSlots; i += 256) keys[i] = EMPTY;
+  if (tid == 0) bad = 0;
+  __syncthreads();
+  uint32_t nb[27];
+  int16_t sl[27];
+  uint32_t mask = 0;
+#pragma unroll
+  for (int v = 0; v < 27; v++) {
+    nb[v] = r < n ? nbr[r * 27 + v] : EMPTY;
+    sl[v] = -1;
+    if (nb[v] == EMPTY) continue;
+    mask |= 1u << v;
+    uint32_t h = (nb[v] * 0x9e3779b1u) >> 22;  // 10 bits: kHaloSlots = 1024
+    for (int probe = 0; probe < kHaloSlots; probe++, h = (h + 1) & (kHaloSlots - 1)) {
+      const uint32_t prev = atomicCAS(&keys[h], EMPTY, nb[v]);
+      if (prev == EMPTY || prev == nb[v]) {
+        sl[v] = (int16_t)h;
+        break;
+      }
+    }
+    if (sl[v] < 0) bad = 1;
+  }
+  __syncthreads();
+  // number the occupied slots: 4 per thread, wave prefix by ballot popcounts, then the 4 wave totals
+  int occ = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) occ += keys[tid * 4 + k] != EMPTY;
+  int incl = occ;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[wv] = incl;
+  __syncthreads();
+  int base = incl - occ;
+  for (int w = 0; w < wv; w++) base += wsum[w];
+  const int U = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int s = tid * 4 + k;
+    pos[s] = base;
+    if (keys[s] != EMPTY) {
+      if (base < UM) rows[t * UM + base] = (int32_t)keys[s];
+      base++;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < 27; v++) {
+    int u = UM;  // EMPTY: the zero row
+    if (sl[v] >= 0) u = min(pos[sl[v]], UM);
+    idx[(t * 27 + v) * B + tid] = (uint16_t)u;
+  }
+  // 16-row group masks
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1) mask |= (uint32_t)__shfl_xor((int)mask, d, 64);
+  if ((tid & 15) == 0) gm[t * (B / 16) + tid / 16] = mask;
+  if (tid == 0) {
+    count[t] = min(U, UM);
+    if (bad || U > UM) atomicMax(overflow, 1);
+  }
+}
+}  // namespace
+
+const SpConvCache::HaloTable& SpConvCache::halo_table() {
+  if (halo) return *halo;
+  auto h = std::make_unique<HaloTable>();
+  const i64 tiles = std::max<i64>(cdiv(N, kHaloRows), 1);
+  h->rows = empty({tiles * kHaloMax}, I32);
+  h->count = empty({tiles}, I32);
+  h->idx = empty({tiles * 27 * kHaloRows / 2}, I32);  // u16 entries
+  h->gm = empty({tiles * (kHaloRows / 16)}, I32);
+  Tensor flag = empty({1}, I32);
+  k_fill_i32<<<1, 64, 0, stream()>>>(flag.ptr<int32_t>(), 1, 0);
+  h->order = window_order(8);  // tiles = 256-row windows of the input order, gray-sorted inside (tight 16-row masks)
+  k_halo_build<<<(unsigned)tiles, 256, 0, stream()>>>(nbr.ptr<uint32_t>(), h->order.ptr<int32_t>(), N,
+                                                       h->rows.ptr<int32_t>(),
+                                                       h->count.ptr<int32_t>(), (uint16_t*)h->idx.p,
+                                                       h->gm.ptr<uint32_t>(), flag.ptr<int32_t>());
+  CK(hipGetLastError());
+  h->ok = to_host_vec<int32_t>(flag)[0] == 0;  // one host sync per cache
+  halo = std::move(h);
+  return *halo;
+}
