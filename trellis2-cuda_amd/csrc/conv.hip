@@ -108,6 +108,8 @@ struct ConvArgs {
   const int32_t* hcount;
   const uint16_t* hidx;
   const uint32_t* hgm;
+  const int32_t* rmap;  // gathered conv through the halo kernel: halo row h reads source row rmap[h] >> rshift
+  int rshift, rmax;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
   uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes, out_bytes, tbl_bytes;
@@ -870,28 +872,28 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   }
 }
 
-// Halo kernel (Ci = Co = 64): a workgroup owns a 256-row window of the input (spatial) order, its rows gray-sorted
-// (SpConvCache::halo_table: tight 16-row neighbour masks, 1.22x the active pairs on C4 against 1.81x unsorted).
-// Before its K
-// loop it copies, by DMA, every distinct neighbour row the tile reads (the tile's halo, ~1.4 rows per output row on
-// shells instead of ~7.7 gathers) into LDS, plus the tile's (row, offset) -> halo index table; the K loop then
-// reads its A operands from LDS with no barriers (each wavefront walks its own offsets) and its weights straight
-// from L2 into registers, one offset ahead. Halo rows are stored with their 16-byte chunks XOR-swizzled by the
-// halo index (conflict-light operand reads); index kHaloMax is a zero row that EMPTY neighbours point at. Two
-// workgroups per CU (LDS 80 KB each): one copies its halo while the other computes. Outputs and residuals are
+// Halo kernel (Co = 64; Ci = 32*S, used at Ci = 64): a workgroup owns a window of B consecutive rows of the input (spatial)
+// order, its rows gray-sorted inside the window (SpConvCache::halo_table: tight 16-row neighbour masks, 1.22x the
+// active pairs on C4 against 1.81x unsorted). Before its K loop it copies, by DMA, every distinct neighbour row the
+// tile reads (the tile's halo, ~1.4 rows per output row on shells instead of ~7 gathers) into LDS, plus the tile's
+// (row, offset) -> halo index table; the K loop then reads its A operands from LDS with no barriers (each wavefront
+// walks its own offsets) and its weights straight from L2 into registers, one offset ahead. Halo rows are stored
+// with their 16-byte chunks XOR-swizzled by the halo index (conflict-light operand reads); index UM is a zero row
+// that EMPTY neighbours point at. With a row map (gathered conv) the halo rows are read through it. Two
+// workgroups per CU (LDS <= 80 KB each): one copies its halo while the other computes. Outputs and residuals are
 // whole rows of the window, permuted inside it.
-template <bool F16, int G, int T>
+template <bool F16, int S, int B, int UM, int G, int T>
 __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
   // wavefront (wr, wc) owns rows wr*16G .. +16G (G groups of 16) x output tiles wc*T .. +T (16 channels each)
-  constexpr int B = SpConvCache::kHaloRows, UM = SpConvCache::kHaloMax, CO = 64, S = 2;
-  constexpr int WC = 4 / T;  // wavefronts across the channels
-  static_assert(4 * 16 * G * T == B * 4, "4 wavefronts cover 256 rows x 4 channel tiles");
-  constexpr int IDXU = 27 * B * 2 / 16;      // 16-byte units of the index table
+  constexpr int CI = 32 * S, RU = CI / 8, CO = 64;  // RU: 16-byte units per feature row
+  constexpr int WC = 4 / T;                         // wavefronts across the channels
+  static_assert((B / (16 * G)) * WC == 4, "4 wavefronts cover B rows x 4 channel tiles");
+  constexpr int IDXU = 27 * B * 2 / 16;        // 16-byte units of the index table
   constexpr int IDXP = (IDXU + 63) / 64 * 64;  // padded to whole wavefront DMA instructions (the tail reads zeros)
-  static_assert(B == 256, "tile shape");
-  __shared__ __attribute__((aligned(16))) u32x4 halo[(UM + 1) * 8];
+  __shared__ __attribute__((aligned(16))) u32x4 halo[(UM + 1) * RU];
   __shared__ __attribute__((aligned(16))) u32x4 idxL[IDXP];
   __shared__ uint32_t gmL[B / 16];
+  static_assert(((UM + 1) * RU + IDXP) * 16 + B / 4 <= 81920, "two workgroups per CU");
   const int g = blockIdx.x, per = a.grid / 8;
   const int tile = (g % 8) * per + g / 8;
   if (tile >= a.tiles_m) return;
@@ -913,15 +915,19 @@ __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
     }
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
     const int32_t* hr = a.hrows + (size_t)tile * UM;
-    const int nins = (U * 8 + 63) / 64;  // wavefront instructions of 64 x 16 bytes (8 halo rows each)
+    const int nins = (U * RU + 63) / 64;  // wavefront instructions of 64 x 16 bytes (64 / RU halo rows each)
     for (int j = wv; j < nins; j += 4) {
-      const int unit = j * 64 + lane, u = unit >> 3, c = unit & 7;
-      const int h = u < U ? hr[u] : -1;
-      const uint32_t off = h >= 0 ? (uint32_t)h * 128u + (uint32_t)((c ^ (u & 7)) * 16) : kOutOfRange;
+      const int unit = j * 64 + lane, u = unit / RU, c = unit % RU;
+      int h = u < U ? hr[u] : -1;
+      if (a.rmap && h >= 0) {  // gathered conv: the halo row is row_map[h] >> shift of the source matrix
+        const uint32_t q = (uint32_t)a.rmap[h] >> a.rshift;
+        h = q < (uint32_t)a.rmax ? (int)q : -1;
+      }
+      const uint32_t off = h >= 0 ? (uint32_t)h * (CI * 2u) + (uint32_t)((c ^ (u & (RU - 1))) * 16) : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)&halo[j * 64], 16, off, 0,
                                                0, 0);
     }
-    if (tid < 8) halo[UM * 8 + tid] = u32x4{0, 0, 0, 0};
+    if (tid < RU) halo[UM * RU + tid] = u32x4{0, 0, 0, 0};
     if (tid < B / 16) gmL[tid] = a.hgm[(size_t)tile * (B / 16) + tid];
   }
   wait_vmcnt<0>();
@@ -929,6 +935,7 @@ __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
 
   // epilogue layout (16-byte row segments, LPR lanes per row) and the output rows, fetched now for later
   constexpr int ES = 16 * T + 4, LPR = 2 * T, RPP = 64 / LPR, NP = 16 / RPP;
+  static_assert(NP >= 1, "a 16-row group spans whole epilogue passes");
   const int c8 = wc * 16 * T + (lane % LPR) * 8;
   int orow[G][NP];
 #pragma unroll
@@ -960,7 +967,8 @@ __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
                                                         0, 0);
   };
   // A operands of offset v for every group (idle groups read the zero row: LDS reads are cheap, and reading them
-  // unconditionally lets the reads of the next offset be issued before this offset's MFMAs)
+  // unconditionally lets the reads of the next offset be issued before this offset's MFMAs). Lane quarter q4 takes
+  // channels (q4*S + m)*8 .. +8 in step m, the weight repack's order.
   auto aload = [&](int v, u32x4 (&av)[G][S]) __attribute__((always_inline)) {
     int u[G];
 #pragma unroll
@@ -968,7 +976,7 @@ __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
 #pragma unroll
     for (int i = 0; i < G; i++)
 #pragma unroll
-      for (int m = 0; m < S; m++) av[i][m] = halo[u[i] * 8 + ((2 * q4 + m) ^ (u[i] & 7))];
+      for (int m = 0; m < S; m++) av[i][m] = halo[u[i] * RU + ((q4 * S + m) ^ (u[i] & (RU - 1)))];
   };
   auto compute = [&](int v, const u32x4 (&w)[T][S], const u32x4 (&av)[G][S]) __attribute__((always_inline)) {
 #pragma unroll
@@ -1009,7 +1017,7 @@ __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
     }
   }
 
-  // epilogue: per 16-row group through a per-wavefront [16][CO+4] fp32 area in the (now idle) halo buffer; the
+  // epilogue: per 16-row group through a per-wavefront [16][16T+4] fp32 area in the (now idle) halo buffer; the
   // output rows (orow, read before the K loop) and every group's residual are requested up front
   __syncthreads();  // every wavefront is done reading the halo
   float* ew = (float*)halo + wv * 16 * ES;
@@ -1046,15 +1054,24 @@ __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
   }
 }
 
-template <bool F16>
+// Halo shapes per input width (rows per tile, halo rows at most, groups and channel tiles per wavefront). Only
+// Ci = 64 is served: at Ci = 128 (C5's children, 128-row windows of 256-byte rows) the kernel was correct but
+// slower than the gathering kernel (1.11 vs 0.91 ms) -- the children's 16-row masks are nearly random, so the
+// MFMA work (2x the active pairs and more) dominates once the gathers are gone.
+template <int S>
+struct HaloShape;
+template <>
+struct HaloShape<2> {  // Ci = 64: 256-row windows, up to 512 halo rows (80 KB of LDS)
+  static constexpr int B = 256, UM = 512, G = 4, T = 4;
+};
+
+template <bool F16, int S>
 void launch_halo(ConvArgs a) {
-  a.tiles_m = cdiv(a.N, SpConvCache::kHaloRows);
+  using H = HaloShape<S>;
+  a.tiles_m = cdiv(a.N, H::B);
   a.tiles_n = 1;
   a.grid = (a.tiles_m + 7) / 8 * 8;
-#ifndef HALO_GT
-#define HALO_GT 4, 4
-#endif
-  k_conv_halo<F16, HALO_GT><<<a.grid, 256, 0, stream()>>>(a);
+  k_conv_halo<F16, S, H::B, H::UM, H::G, H::T><<<a.grid, 256, 0, stream()>>>(a);
 }
 
 template <bool F16, int S, int T>
@@ -1334,7 +1351,7 @@ void dispatch(const SpConvCfg& cfg, ConvArgs a) {
   // The fp16-compatible epilogue runs in the generic kernel only: its longer rounding sequence (IEEE quotient,
   // accurate exp) would cost the tuned kernels registers in their epilogues.
   const bool compat = a.act & EPI_F16_COMPAT;
-  if (a.hrows) return launch_halo<F16>(a);
+  if (a.hrows) return launch_halo<F16, 2>(a);
   if (!compat && a.Co == 64 && a.Ci <= 128) {
     switch (a.Ci / 32) {
       case 1: return launch_narrow<F16, 1, 4>(a);
@@ -1458,8 +1475,8 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   const bool compat = act & EPI_F16_COMPAT;
   const i64 chunks = (i64)Co * 27 * Ci / 8;
   const SpConvCache::HaloTable* ht = nullptr;
-  if (!compat && !row_map && Co == 64 && Ci == 64 && halo_enabled()) {
-    ht = &c.halo_table();
+  if (!compat && Co == 64 && Ci == 64 && halo_enabled()) {
+    ht = &c.halo_table(HaloShape<2>::B, HaloShape<2>::UM);
     if (!ht->ok) ht = nullptr;
   }
   if (ht) {  // halo kernel: narrow weight order, the tile's distinct neighbour rows copied to LDS once
@@ -1471,6 +1488,11 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     a.hidx = (const uint16_t*)ht->idx.p;
     a.hgm = ht->gm.ptr<uint32_t>();
     a.order = ht->order.ptr<int32_t>();
+    if (row_map) {
+      a.rmap = row_map->ptr<int32_t>();
+      a.rshift = shift;
+      a.rmax = (int)std::min<i64>(M, INT32_MAX);
+    }
   } else if (!compat && Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, spatial row order
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);

@@ -483,25 +483,26 @@ __global__ void k_fill_i32(int32_t* __restrict__ p, i64 n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
-// One workgroup per tile of kHaloRows input-order rows, one thread per row. The tile's neighbour rows go into an
-// LDS open-addressed set (linear probing, at most kHaloSlots probes: a tile with more distinct rows is flagged);
-// occupied slots are then numbered by a workgroup prefix count, which gives the halo list and every (row, offset)
-// its index in it. The list order follows the slots (not deterministic under concurrent inserts) -- only where a
-// row sits in the conv's LDS copy depends on it, never a sum.
-__global__ void __launch_bounds__(256) k_halo_build(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ order,
-                                                    i64 n, int32_t* __restrict__ rows,
-                                                    int32_t* __restrict__ count, uint16_t* __restrict__ idx,
-                                                    uint32_t* __restrict__ gm, int32_t* __restrict__ overflow) {
-  constexpr int B = SpConvCache::kHaloRows, UM = SpConvCache::kHaloMax;
-  static_assert(B == 256, "one thread per row");
+// One workgroup per tile of B rows (positions of the tile order), one thread per row. The tile's neighbour rows go
+// into an LDS open-addressed set (linear probing, at most kHaloSlots probes: a tile with more distinct rows is
+// flagged); occupied slots are then numbered by a workgroup prefix count, which gives the halo list and every
+// (row, offset) its index in it. The list order follows the slots (not deterministic under concurrent inserts) --
+// only where a row sits in the conv's LDS copy depends on it, never a sum.
+template <int B, int UM>
+__global__ void __launch_bounds__(B) k_halo_build(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ order,
+                                                  i64 n, int32_t* __restrict__ rows, int32_t* __restrict__ count,
+                                                  uint16_t* __restrict__ idx, uint32_t* __restrict__ gm,
+                                                  int32_t* __restrict__ overflow) {
+  constexpr int NWV = B / 64, SPT = kHaloSlots / B;  // wavefronts, slots per thread
+  static_assert(B % 64 == 0 && B <= 256 && UM < 65535 && 2 * UM <= kHaloSlots, "halo tile shape");
   __shared__ uint32_t keys[kHaloSlots];
   __shared__ int pos[kHaloSlots];
-  __shared__ int wsum[4];
+  __shared__ int wsum[NWV];
   __shared__ int bad;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const i64 t = blockIdx.x, p = t * B + tid;  // position in the tile order; its row is order[p]
   const i64 r = p < n ? order[p] : n;
-  for (int i = tid; i < kHaloSlots; i += 256) keys[i] = EMPTY;
+  for (int i = tid; i < kHaloSlots; i += B) keys[i] = EMPTY;
   if (tid == 0) bad = 0;
   __syncthreads();
   uint32_t nb[27];
@@ -524,10 +525,10 @@ __global__ void __launch_bounds__(256) k_halo_build(const uint32_t* __restrict__
     if (sl[v] < 0) bad = 1;
   }
   __syncthreads();
-  // number the occupied slots: 4 per thread, wave prefix by ballot popcounts, then the 4 wave totals
+  // number the occupied slots: SPT per thread, wave prefix by shuffles, then the wave totals
   int occ = 0;
 #pragma unroll
-  for (int k = 0; k < 4; k++) occ += keys[tid * 4 + k] != EMPTY;
+  for (int k = 0; k < SPT; k++) occ += keys[tid * SPT + k] != EMPTY;
   int incl = occ;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -536,12 +537,14 @@ __global__ void __launch_bounds__(256) k_halo_build(const uint32_t* __restrict__
   }
   if (lane == 63) wsum[wv] = incl;
   __syncthreads();
-  int base = incl - occ;
-  for (int w = 0; w < wv; w++) base += wsum[w];
-  const int U = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  int base = incl - occ, U = 0;
+  for (int w = 0; w < NWV; w++) {
+    if (w < wv) base += wsum[w];
+    U += wsum[w];
+  }
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int s = tid * 4 + k;
+  for (int k = 0; k < SPT; k++) {
+    const int s = tid * SPT + k;
     pos[s] = base;
     if (keys[s] != EMPTY) {
       if (base < UM) rows[t * UM + base] = (int32_t)keys[s];
@@ -566,23 +569,29 @@ __global__ void __launch_bounds__(256) k_halo_build(const uint32_t* __restrict__
 }
 }  // namespace
 
-const SpConvCache::HaloTable& SpConvCache::halo_table() {
-  if (halo) return *halo;
-  auto h = std::make_unique<HaloTable>();
-  const i64 tiles = std::max<i64>(cdiv(N, kHaloRows), 1);
-  h->rows = empty({tiles * kHaloMax}, I32);
-  h->count = empty({tiles}, I32);
-  h->idx = empty({tiles * 27 * kHaloRows / 2}, I32);  // u16 entries
-  h->gm = empty({tiles * (kHaloRows / 16)}, I32);
+const SpConvCache::HaloTable& SpConvCache::halo_table(int B, int UM) {
+  auto it = halo.find({B, UM});
+  if (it != halo.end()) return it->second;
+  HaloTable h;
+  const i64 tiles = std::max<i64>(cdiv(N, B), 1);
+  int log2b = 0;
+  while ((1 << log2b) < B) log2b++;
+  REQ((1 << log2b) == B, "halo tile rows %d: a power of two", B);
+  h.order = window_order(log2b);  // B-row windows of the input order, gray-sorted inside (tight 16-row masks)
+  h.rows = empty({tiles * UM}, I32);
+  h.count = empty({tiles}, I32);
+  h.idx = empty({tiles * 27 * B / 2}, I32);  // u16 entries
+  h.gm = empty({tiles * (B / 16)}, I32);
   Tensor flag = empty({1}, I32);
   k_fill_i32<<<1, 64, 0, stream()>>>(flag.ptr<int32_t>(), 1, 0);
-  h->order = window_order(8);  // tiles = 256-row windows of the input order, gray-sorted inside (tight 16-row masks)
-  k_halo_build<<<(unsigned)tiles, 256, 0, stream()>>>(nbr.ptr<uint32_t>(), h->order.ptr<int32_t>(), N,
-                                                       h->rows.ptr<int32_t>(),
-                                                       h->count.ptr<int32_t>(), (uint16_t*)h->idx.p,
-                                                       h->gm.ptr<uint32_t>(), flag.ptr<int32_t>());
+  auto go = [&](auto kern) {
+    kern<<<(unsigned)tiles, B, 0, stream()>>>(nbr.ptr<uint32_t>(), h.order.ptr<int32_t>(), N, h.rows.ptr<int32_t>(),
+                                              h.count.ptr<int32_t>(), (uint16_t*)h.idx.p, h.gm.ptr<uint32_t>(),
+                                              flag.ptr<int32_t>());
+  };
+  if (B == 256 && UM == 512) go(k_halo_build<256, 512>);
+  else REQ(false, "no halo builder for B=%d UM=%d", B, UM);
   CK(hipGetLastError());
-  h->ok = to_host_vec<int32_t>(flag)[0] == 0;  // one host sync per cache
-  halo = std::move(h);
-  return *halo;
+  h.ok = to_host_vec<int32_t>(flag)[0] == 0;  // one host sync per cache and shape
+  return halo.emplace(std::make_pair(B, UM), h).first->second;
 }

@@ -4,8 +4,6 @@
 #include <map>
 #include <utility>
 
-#include <memory>
-
 #include "core.h"
 
 // Neighbour cache for one coordinate set (reference src/spconv.h:5-11).
@@ -41,20 +39,18 @@ struct SpConvCache {
   // row_table(log2w).tbl with every non-EMPTY entry r replaced by row_map[r] >> shift, or EMPTY when that is not
   // below m (not memoized: row_map is the caller's). Used by the gathered conv.
   Tensor mapped_table(int log2w, const Tensor& row_map, int shift, i64 m);
-  // Halo schedule for the 64-channel conv (tiles of kHaloRows consecutive entries of order = window_order(8), i.e.
-  // 256-row windows of the input order, gray-sorted inside): per tile the distinct
-  // neighbour rows it reads (rows[t*kHaloMax + u], u < count[t]), each row's 27 neighbours as indices into that
-  // list (idx[(t*27 + v)*kHaloRows + j] for position j of the tile, u16; kHaloMax = EMPTY, a zero row) and the
-  // per-16-position neighbour masks
-  // (gm[t*kHaloRows/16 + g]). ok = false when some tile reads more than kHaloMax distinct rows (its conv then uses
-  // the gathering kernel). Built on first use (one host sync for ok) and memoized.
-  static constexpr int kHaloRows = 256, kHaloMax = 512;
+  // Halo schedule for the 64-output-channel convs: tiles of B consecutive entries of order = window_order(log2 B)
+  // (B-row windows of the input order, gray-sorted inside). Per tile: the distinct neighbour rows it reads
+  // (rows[t*UM + u], u < count[t]), each position's 27 neighbours as indices into that list (idx[(t*27 + v)*B + j],
+  // u16; UM = EMPTY, a zero row) and the per-16-position neighbour masks (gm[t*B/16 + g]). ok = false when a tile
+  // reads more than UM distinct rows (its conv then uses the gathering kernel). Built on first use per (B, UM), one
+  // host sync for ok, memoized.
   struct HaloTable {
     Tensor order, rows, count, idx, gm;
     bool ok = false;
   };
-  std::unique_ptr<HaloTable> halo;
-  const HaloTable& halo_table();
+  std::map<std::pair<int, int>, HaloTable> halo;
+  const HaloTable& halo_table(int B, int UM);
   // The brick hash, kept when built with keep_hash (for coordinate lookups by other consumers): slot table,
   // brick records, slot mask and the grid bounds.
   Tensor htable, hbricks;
