@@ -882,8 +882,8 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 // that EMPTY neighbours point at. With a row map (gathered conv) the halo rows are read through it. Two
 // workgroups per CU (LDS <= 80 KB each): one copies its halo while the other computes. Outputs and residuals are
 // whole rows of the window, permuted inside it.
-template <bool F16, int S, int B, int UM, int G, int T>
-__global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
+template <bool F16, int S, int B, int UM, int G, int T, int OCC>
+__global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
   // wavefront (wr, wc) owns rows wr*16G .. +16G (G groups of 16) x output tiles wc*T .. +T (16 channels each)
   constexpr int CI = 32 * S, RU = CI / 8, CO = 64;  // RU: 16-byte units per feature row
   constexpr int WC = 4 / T;                         // wavefronts across the channels
@@ -893,7 +893,7 @@ __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
   __shared__ __attribute__((aligned(16))) u32x4 halo[(UM + 1) * RU];
   __shared__ __attribute__((aligned(16))) u32x4 idxL[IDXP];
   __shared__ uint32_t gmL[B / 16];
-  static_assert(((UM + 1) * RU + IDXP) * 16 + B / 4 <= 81920, "two workgroups per CU");
+  static_assert((((UM + 1) * RU + IDXP) * 16 + B / 4) * OCC <= 163840, "OCC workgroups per CU");
   const int g = blockIdx.x, per = a.grid / 8;
   const int tile = (g % 8) * per + g / 8;
   if (tile >= a.tiles_m) return;
@@ -1061,8 +1061,8 @@ __global__ void __launch_bounds__(256, 2) k_conv_halo(ConvArgs a) {
 template <int S>
 struct HaloShape;
 template <>
-struct HaloShape<2> {  // Ci = 64: 256-row windows, up to 512 halo rows (80 KB of LDS)
-  static constexpr int B = 256, UM = 512, G = 4, T = 4;
+struct HaloShape<2> {  // Ci = 64: 256-row windows, up to 512 halo rows (80 KB of LDS, two workgroups per CU)
+  static constexpr int B = 256, UM = 512, G = 4, T = 4, OCC = 2;
 };
 
 template <bool F16, int S>
@@ -1071,7 +1071,7 @@ void launch_halo(ConvArgs a) {
   a.tiles_m = cdiv(a.N, H::B);
   a.tiles_n = 1;
   a.grid = (a.tiles_m + 7) / 8 * 8;
-  k_conv_halo<F16, S, H::B, H::UM, H::G, H::T><<<a.grid, 256, 0, stream()>>>(a);
+  k_conv_halo<F16, S, H::B, H::UM, H::G, H::T, H::OCC><<<a.grid, 256, 0, stream()>>>(a);
 }
 
 template <bool F16, int S, int T>
