@@ -263,3 +263,14 @@ def test_f16_compat_epilogue(gpu, ci, co):
                 assert torch.all(d[bad] <= torch.from_numpy(tol)), what
     with pytest.raises(RuntimeError):  # bf16 is not a compat dtype
         sp.subm_conv_fused(xs.bfloat16(), ws.bfloat16(), None, cache, act=sp.EPI_F16_COMPAT)
+
+
+def test_halo_fallback_shuffled_rows(gpu):
+    """64 -> 64 on a shell whose rows are shuffled: every 256-row window then reads far more than 512 distinct
+    neighbour rows, so the halo schedule reports overflow and the conv runs on the gathering kernel -- same
+    results either way (checked against the oracle); the unshuffled shell takes the halo kernel."""
+    c = shell(12.0)
+    rng = np.random.default_rng(4)
+    shuffled = c[rng.permutation(len(c))]
+    for coords in (c, shuffled):
+        run_case(gpu, coords, 64, 64, res_dt="bf16")
