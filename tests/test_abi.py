@@ -51,3 +51,29 @@ def test_no_oracle_in_product():
                 src = open(os.path.join(dp, f)).read()
                 assert "import oracle" not in src and "liboracle" not in src and "orc_" not in src, f
     assert "orc_" not in os.popen(f"nm -D {spconv_amd.LIB_PATH}").read()
+
+
+def test_header_is_plain_c_and_links(tmp_path):
+    """include/spconv_amd.h compiles as C99 and a C program that calls host-only entry points links against the
+    library and runs without a GPU (the header is what a cgo / JNI / N-API binding would include)."""
+    src = tmp_path / "abi.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include "spconv_amd.h"
+int main(void) {
+  int b1, bk, s;
+  if (spc_conv_cfg(1000, 64, 64, &b1, &bk, &s) != 0) return 1;
+  if (spc_conv_cfg_autotune("/nonexistent.json", "NVIDIA H200", 1000, 64, 64, &b1, &bk, &s) == 0) return 2;
+  if (spc_last_error() == 0 || spc_last_error()[0] == 0) return 3;
+  if (spc_subm_conv(0, 0, 0, SPC_BF16, SPC_F32, 10, 64, 64, 0, 0) == 0) return 4;  /* null cache: an error */
+  printf("%d %d %d\n", b1, bk, s);
+  return 0;
+}
+''')
+    exe = tmp_path / "abi"
+    libdir = os.path.dirname(spconv_amd.LIB_PATH)
+    cmd = (f"gcc -std=c99 -Wall -Werror -I{ROOT}/include {src} -o {exe} -L{libdir} -lspconv_amd "
+           f"-Wl,-rpath,{libdir}")
+    assert os.system(cmd) == 0, cmd
+    out = os.popen(str(exe)).read()
+    assert out.strip() == "128 64 1"
