@@ -226,6 +226,9 @@ def main():
             sp.subm_conv_fused(sp.gather_ln_act(h1, src, 0), w2, b2, c2, out=y2)
             sp.add_skip(y2, xp, src)
 
+        def half_fused_skip():
+            sp.subm_conv_skip(sp.gather_ln_act(h1, src, 0), w2, b2, c2, xp, src, out=y2)
+
         def half_gathered_conv():
             sp.subm_conv_gathered(sp.gather_ln_act(h1), src, 0, w2, b2, c2, out=y2)
             sp.add_skip(y2, xp, src)
@@ -236,6 +239,7 @@ def main():
         e2e["second_half"] = {
             "children": len(ch), "Co": co2,
             "gather_ln_silu_then_conv_ms": round(timed(half_gathered_rows, 10), 4),
+            "gather_ln_silu_then_conv_skip_fused_ms": round(timed(half_fused_skip, 10), 4),
             "ln_silu_parents_then_gathered_conv_ms": round(timed(half_gathered_conv, 10), 4),
             "gather_ln_silu_ms": round(timed(lambda: sp.gather_ln_act(h1, src, 0), 20), 4),
             "torch_gather_ln_silu_ms": round(timed(torch_preact, 20), 4),

@@ -125,6 +125,15 @@ int spc_convnext_mlp(const void* h, const void* x, const void* gamma, const void
                      const void* b1, const void* w2, const void* b2, int dtype, int param_dtype, int64_t N, int C,
                      void* y);
 
+/* Conv and the upsample block's skip connection in one pass: out = act(conv(x, w) + b) + skip with skip[i,c] =
+ * x_skip[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep], rep = Co / (Cin/8) a power of two; fp32 sum, one rounding.
+ * x [N,Ci], w [Co,27,Ci], x_skip [n_skip,Cin] (Cin % 64 == 0), out [N,Co]: one 16-bit `dtype`; src int32 [N] (the
+ * c2s output). Fused into the 64 -> 64 kernel; other shapes run the conv and spc_add_skip's pass.
+ * Replaces: subm_conv + k_add_skip of SDecoder::up (src/sdec.cu:38-43, 82-84). */
+int spc_subm_conv_skip(const void* x, const void* w, const void* b, int dtype, int b_dtype, int act,
+                       const void* x_skip, int64_t n_skip, int Cin, const int32_t* src, int64_t N, int Ci, int Co,
+                       spc_cache* c, void* out);
+
 /* Skip connection of the upsample block, in place: h[i,c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep] with
  * rep = Co / (Cin/8), the fp32 sum rounded once to `dtype` (bit-identical to the reference); h [m,Co], x [n,Cin],
  * both SPC_F16 or SPC_BF16, 16-byte aligned; Cin % 8 == 0, Co % 8 == 0, Co % (Cin/8) == 0. src entries outside

@@ -162,3 +162,38 @@ def test_upsample_block(gpu):
     rel = np.linalg.norm(yr - ref) / np.linalg.norm(ref)
     err = np.abs(yr - ref)
     assert rel <= 3e-3 and np.all(err <= np.maximum(2e-2, 2 * ulp(ref, torch.bfloat16))), (rel, err.max())
+    # (c) conv2 and the skip add in one pass (one rounding instead of two): same bar against the fp32 chain
+    yc = sp.subm_conv_skip(sp.gather_ln_act(h1g, src, 0), wg, bg, cache, xg, src).float().cpu().numpy()
+    ref32 = y32.float().numpy() + (skip_reference(torch.zeros_like(y32), x, src.cpu()).float().numpy())
+    relc = np.linalg.norm(yc - ref32) / np.linalg.norm(ref32)
+    errc = np.abs(yc - ref32)
+    assert relc <= 3e-3 and np.all(errc <= np.maximum(2e-2, 2 * ulp(ref32, torch.bfloat16))), (relc, errc.max())
+
+
+@pytest.mark.parametrize("Cin,Ci", [(64, 64), (128, 64), (256, 64), (512, 64), (128, 128)])
+def test_conv_skip(gpu, Cin, Ci):
+    """subm_conv_skip (rep = 8, 4, 2, 1 on the fused 64 -> 64 path; Ci = 128 runs conv then add_skip) against the
+    fp32 oracle conv plus the skip in fp32, rounded once: the conv's bf16 bar."""
+    import oracle
+    from spconv_amd import workloads as W
+    par = W.shell_coords(W.CONFIGS["c1"])
+    n, Co = len(par), 64
+    ch, src = sp.subdivide(torch.from_numpy(par).to(gpu),
+                           torch.from_numpy(W.keep_logits(n, 0.4, 8).view(np.int16)).to(gpu).view(torch.float16))
+    m = len(ch)
+    print(f"conv_skip case Cin={Cin} Ci={Ci} children={m}", flush=True)
+    g = torch.Generator().manual_seed(Cin + Ci)
+    x = torch.randn((m, Ci), generator=g).to(torch.bfloat16)
+    xs = torch.randn((n, Cin), generator=g).to(torch.bfloat16)
+    w, b = W.conv_params(W.Config("t", 0, 0, (0, 0), False, 0, Ci, Co, "bf16", "", 41))
+    wq = torch.from_numpy(w).to(torch.bfloat16)
+    cache = sp.build_neighbors(ch.contiguous())
+    for act in (0, 1):
+        y = sp.subm_conv_skip(x.to(gpu), wq.to(gpu), torch.from_numpy(b).to(gpu), cache, xs.to(gpu), src, act=act)
+        nbr, _, _, _ = oracle.build_neighbors(ch.cpu().numpy())
+        conv = oracle.conv(x.float().numpy(), wq.float().numpy(), b, nbr, act=act)
+        ref = conv + skip_reference(torch.zeros((m, Co), dtype=torch.bfloat16), xs, src.cpu()).float().numpy()
+        yr = y.float().cpu().numpy()
+        rel = np.linalg.norm(yr - ref) / np.linalg.norm(ref)
+        err = np.abs(yr - ref)
+        assert rel <= 3e-3 and np.all(err <= np.maximum(2e-2, ulp(ref, torch.bfloat16))), (act, rel, err.max())

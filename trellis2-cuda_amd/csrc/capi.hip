@@ -194,6 +194,24 @@ SPC_API int spc_convnext_mlp(const void* h, const void* x, const void* gamma, co
   });
 }
 
+SPC_API int spc_subm_conv_skip(const void* x, const void* w, const void* b, int dtype, int b_dtype, int act,
+                               const void* x_skip, int64_t n_skip, int Cin, const int32_t* src, int64_t N, int Ci,
+                               int Co, spc_cache* c, void* out) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    REQ(N == c->c.N, "N=%lld but the cache has %d rows", (long long)N, c->c.N);
+    REQ(n_skip >= 0 && Cin > 0 && Ci > 0 && Co > 0, "n_skip=%lld Cin=%d Ci=%d Co=%d", (long long)n_skip, Cin, Ci, Co);
+    DT dt = float_dt(dtype, "x/w/x_skip/out");
+    REQ(dt != F32, "x/w/x_skip/out must be fp16 or bf16");
+    if (N == 0) return;
+    REQ(x && w && x_skip && src && out && n_skip > 0, "null x/w/x_skip/src/out or n_skip = 0");
+    Tensor tx = borrow(x, {N, Ci}, dt), tw = borrow(w, {Co, 27, Ci}, dt), ts = borrow(x_skip, {n_skip, Cin}, dt);
+    Tensor tsrc = borrow(src, {N}, I32), to = borrow(out, {N, Co}, dt), tb;
+    if (b) tb = borrow(b, {Co}, float_dt(b_dtype, "bias"));
+    subm_conv_skip(tx, tw, b ? &tb : nullptr, act, ts, tsrc, c->c, to);
+  });
+}
+
 SPC_API int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, int Co, int64_t n, int Cin,
                          int dtype) {
   return guarded([&] {

@@ -110,6 +110,12 @@ struct ConvArgs {
   const uint32_t* hgm;
   const int32_t* rmap;  // gathered conv through the halo kernel: halo row h reads source row rmap[h] >> rshift
   int rshift, rmax;
+  // skip residual (upsample block, halo kernel only): residual[i, c] = skip_x[src[i] >> 3, (src[i] & 7) * Cin/8 +
+  // c / rep] with src = skip_src, Cin = skip_cin, rep = skip_rep (a power of two)
+  const uint16_t* skip_x;
+  const int32_t* skip_src;
+  int skip_cin, skip_rep;
+  uint32_t skip_bytes, skip_n;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
   uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes, out_bytes, tbl_bytes;
@@ -872,6 +878,31 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   }
 }
 
+// 8 consecutive channels c8.. of the skip residual of one output row, as 8 x 16-bit in r (src < 0 or past the
+// source rows: zeros). Channel c reads element c / rep of the parent's slot, so 8 channels need 8 / rep elements
+// (one for rep >= 8): one 16-, 8-, 4- or 2-byte load, widened by repeating each element rep times.
+__device__ __forceinline__ u32x4 load_skip8(const __amdgpu_buffer_rsrc_t& rs, const ConvArgs& a, int src, int c8,
+                                            bool ok) {
+  const uint32_t s = (uint32_t)src;
+  const bool live = ok && s < a.skip_n * 8u;
+  const uint32_t base = (s >> 3) * (uint32_t)a.skip_cin + (s & 7u) * (uint32_t)(a.skip_cin >> 3) +
+                        (uint32_t)(c8 / a.skip_rep);
+  const uint32_t off = live ? base * 2u : kOutOfRange;
+  auto dup = [](uint32_t v16) { return (v16 & 0xffffu) | (v16 << 16); };
+  if (a.skip_rep == 1) return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+  if (a.skip_rep == 2) {
+    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+    const u32x2v q = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    return u32x4{dup(q[0]), dup(q[0] >> 16), dup(q[1]), dup(q[1] >> 16)};
+  }
+  if (a.skip_rep == 4) {
+    const uint32_t q = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    return u32x4{dup(q), dup(q), dup(q >> 16), dup(q >> 16)};
+  }
+  const uint32_t q = dup(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+  return u32x4{q, q, q, q};
+}
+
 // Halo kernel (Co = 64; Ci = 32*S, used at Ci = 64): a workgroup owns a window of B consecutive rows of the input (spatial)
 // order, its rows gray-sorted inside the window (SpConvCache::halo_table: tight 16-row neighbour masks, 1.22x the
 // active pairs on C4 against 1.81x unsorted). Before its K loop it copies, by DMA, every distinct neighbour row the
@@ -945,6 +976,12 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
       const int pos = row0 + wr * 16 * G + i * 16 + p * RPP + lane / LPR;
       orow[i][p] = pos < N ? a.order[pos] : 0;
     }
+  int ssrc[G][NP];  // skip residual: the output rows' c2s entries (row orow reads its parent slot)
+  if (a.skip_src)
+#pragma unroll
+    for (int i = 0; i < G; i++)
+#pragma unroll
+      for (int p = 0; p < NP; p++) ssrc[i][p] = a.skip_src[orow[i][p]];
   uint32_t gms[G], wmask = 0;
 #pragma unroll
   for (int i = 0; i < G; i++) {
@@ -1030,7 +1067,15 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
   for (int i = 0; i < G; i++)
 #pragma unroll
     for (int p = 0; p < NP; p++)
-      load_res8(e, (uint32_t)orow[i][p] * CO + c8, row0 + wr * 16 * G + i * 16 + p * RPP + lane / LPR < N, resv[i][p]);
+    {
+      const bool ok = row0 + wr * 16 * G + i * 16 + p * RPP + lane / LPR < N;
+      if (a.skip_src) {
+        resv[i][p][0] = load_skip8(make_rsrc(a.skip_x, a.skip_bytes), a, ssrc[i][p], c8, ok);
+        resv[i][p][1] = u32x4{0, 0, 0, 0};
+      } else {
+        load_res8(e, (uint32_t)orow[i][p] * CO + c8, ok, resv[i][p]);
+      }
+    }
 #pragma unroll
   for (int i = 0; i < G; i++) {
 #pragma unroll
@@ -1404,8 +1449,12 @@ bool halo_enabled() {
 }
 
 // x: the conv input [N,Ci], or with row_map the source rows [M,Ci] read through row_map >> shift
+struct SkipRes {  // skip residual of the upsample block (see ConvArgs::skip_*)
+  const Tensor* x;
+  const Tensor* src;
+};
 void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& w, const Tensor* b,
-               const Tensor* residual, int act, SpConvCache& c, Tensor& out) {
+               const Tensor* residual, int act, SpConvCache& c, Tensor& out, const SkipRes* skip = nullptr) {
   REQ(x.dim() == 2 && w.dim() == 3, "x must be [N,Ci], w [Co,27,Ci]");
   const int N = row_map ? c.N : (int)x.size(0), Ci = (int)x.size(1), Co = (int)w.size(0);
   const i64 M = x.size(0);
@@ -1493,6 +1542,17 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       a.rshift = shift;
       a.rmax = (int)std::min<i64>(M, INT32_MAX);
     }
+    if (skip) {
+      a.skip_x = skip->x->ptr<uint16_t>();
+      a.skip_src = skip->src->ptr<int32_t>();
+      a.skip_cin = (int)skip->x->size(1);
+      a.skip_rep = Co / (a.skip_cin / 8);
+      a.skip_n = (uint32_t)skip->x->size(0);
+      a.skip_bytes = (uint32_t)skip->x->bytes();
+      a.res = skip->x->p;  // the epilogue's residual type (16-bit); its rows come through load_skip8
+      a.res_dt = skip->x->dt;
+      a.res_bytes = a.skip_bytes;
+    }
   } else if (!compat && Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, spatial row order
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
@@ -1515,9 +1575,32 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       a.tbl_bytes = (uint32_t)rt.tbl.bytes();
     }
   }
+  REQ(!skip || ht, "the fused skip residual needs the halo kernel");
   if (x.dt == F16) dispatch<true>(cfg, a);
   else dispatch<false>(cfg, a);
   CK(hipGetLastError());
+}
+
+void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, const Tensor& x_skip,
+                    const Tensor& src, SpConvCache& c, Tensor& out) {
+  REQ(x.dim() == 2 && w.dim() == 3 && x_skip.dim() == 2, "x [N,Ci], w [Co,27,Ci], x_skip [n,Cin]");
+  const int Ci = (int)x.size(1), Co = (int)w.size(0), Cin = (int)x_skip.size(1);
+  REQ(src.dt == I32 && src.numel() == c.N, "src must be int32 [%d]", c.N);
+  REQ(x_skip.dt == out.dt && (out.dt == BF16 || out.dt == F16), "x_skip and out: one 16-bit dtype");
+  REQ(Cin % 64 == 0 && Co % (Cin / 8) == 0, "Cin=%d Co=%d: need Cin %% 64 == 0 and Co a multiple of Cin/8", Cin, Co);
+  const int rep = Co / (Cin / 8);
+  REQ((rep & (rep - 1)) == 0, "Co / (Cin/8) = %d must be a power of two", rep);
+  REQ((uint64_t)x_skip.bytes() <= kMaxBufferBytes && ((uintptr_t)x_skip.p % 16) == 0, "x_skip too large / unaligned");
+  REQ(!(act & EPI_F16_COMPAT), "no fp16-compatible epilogue with the fused skip");
+  bool fused = c.N > 0 && Ci == 64 && Co == 64 && halo_enabled();
+  if (fused) fused = c.halo_table(HaloShape<2>::B, HaloShape<2>::UM).ok;
+  if (fused) {
+    const SkipRes sk{&x_skip, &src};
+    conv_impl(x, nullptr, 0, w, b, nullptr, act, c, out, &sk);
+  } else {  // other shapes: the conv, then the skip add as its own pass
+    conv_impl(x, nullptr, 0, w, b, nullptr, act, c, out);
+    add_skip(out, x_skip, src);
+  }
 }
 
 void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Tensor* residual, int act,

@@ -120,6 +120,13 @@ void gather_ln_act(const Tensor& x_src, const Tensor* row_map, int shift, const 
 void convnext_mlp(const Tensor& h, const Tensor& x, const Tensor* gamma, const Tensor* beta, float eps, const Tensor& w1,
                   const Tensor* b1, const Tensor& w2, const Tensor* b2, Tensor& y);
 
+// Conv plus the upsample block's skip connection in one pass: out = act(conv(x) + b) + skip, skip[i, c] =
+// x_skip[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep], rep = Co / (Cin/8) a power of two, one rounding (reference:
+// subm_conv then k_add_skip, src/sdec.cu:38-43, 82-84). Fused into the 64 -> 64 halo kernel; other shapes run the
+// conv and then add_skip. out and x_skip share a 16-bit dtype.
+void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, const Tensor& x_skip,
+                    const Tensor& src, SpConvCache& c, Tensor& out);
+
 // Skip connection of the upsample block, in place (reference k_add_skip, src/sdec.cu:38-43):
 // h[i, c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep], rep = Co / (Cin/8), fp32 sum rounded once (bit-identical
 // to the reference). h [m,Co] and x [n,Cin] of one dtype (fp16/bf16); entries of src outside x leave the row.

@@ -28,7 +28,8 @@ EMPTY = 0xFFFFFFFF
 SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build_neighbors_ex", "spc_cache_lookup",
            "spc_fdg_quads", "spc_cache_free", "spc_cache_info", "spc_cache_valid", "spc_conv_cfg",
            "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
-           "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subdivide")
+           "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subm_conv_skip",
+           "spc_subdivide")
 
 _lib = None
 
@@ -62,6 +63,7 @@ def load_library():
     L.spc_gather_ln_act.argtypes = [P, I64, I, P, I, P, P, ctypes.c_float, I, I, I64, P]
     L.spc_add_skip.argtypes = [P, P, P, I64, I, I64, I, I]
     L.spc_convnext_mlp.argtypes = [P, P, P, P, ctypes.c_float, P, P, P, P, I, I, I64, I, P]
+    L.spc_subm_conv_skip.argtypes = [P, P, P, I, I, I, P, I64, I, P, I64, I, I, P, P]
     L.spc_subdivide.argtypes = [P, P, I64, P, P, ctypes.POINTER(I64)]
     for name in SYMBOLS:
         if name != "spc_last_error":
@@ -289,6 +291,22 @@ def convnext_mlp(h, x, gamma, beta, w1, b1, w2, b2, eps: float = 1e-6, out=None)
     _check(load_library().spc_convnext_mlp(_ptr(h), _ptr(x), _ptr(gamma), _ptr(beta), eps, _ptr(w1), _ptr(b1),
                                            _ptr(w2), _ptr(b2), _dt(h), _dt(ps[0]) if ps else F32, N, C,
                                            _ptr(out)))
+    return out
+
+
+def subm_conv_skip(x, w, b, cache: SpConvCache, x_skip, src, act: int = ACT_NONE, out=None):
+    """act(subm_conv3d(x, w) + b) + repeat_interleave(C2S(x_skip), Co / (Cin/8), dim=1) in one pass (the reference's
+    conv2 + k_add_skip of SDecoder::up, src/sdec.cu:38-43, 82-84); out has x's 16-bit dtype."""
+    torch = _torch()
+    N, Ci = x.shape
+    Co = w.shape[0]
+    n_skip, Cin = x_skip.shape
+    if src.dtype != torch.int32 or src.numel() != N:
+        raise ValueError(f"src must be int32 [{N}]")
+    if out is None:
+        out = torch.empty((N, Co), dtype=x.dtype, device=x.device)
+    _check(load_library().spc_subm_conv_skip(_ptr(x), _ptr(w), _ptr(b), _dt(x), _dt(b) if b is not None else F32, act,
+                                             _ptr(x_skip), n_skip, Cin, _ptr(src), N, Ci, Co, cache._h, _ptr(out)))
     return out
 
 
