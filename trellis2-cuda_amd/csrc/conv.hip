@@ -1137,16 +1137,19 @@ void launch_narrow(ConvArgs a) {
 //  * Ring protocol per stage s: wait (counted vmcnt) for this lane's DMA of A(s), barrier (every wavefront's
 //    part has landed and everyone is done with stage s-1), then, between the MFMA groups of stage s, refill the
 //    slot stage s-1 used with A(s+3) and load the weights of stage s+1 into the other register set.
-template <bool F16, int BM>
-__global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvArgs a) {
-  constexpr int NW = 4, NT = 256, KC = 64, PC = KC / 8;
-  constexpr int TM = BM / 32, TN = 2, AL = BM * PC / NT;  // AL = TM DMA loads per lane per stage
-  constexpr int BQ = 8 / TM;                            // weight loads per 32-row group (8 per stage)
+template <bool F16, int BM, int RS>
+__global__ void __launch_bounds__(256 * RS, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvArgs a) {
+  // RS = 1: 4 wavefronts, each all BM rows x 64 channels. RS = 2: 8 wavefronts (two per SIMD), wavefront (wr, wn)
+  // owns rows wr*BM/2 .. +BM/2 x channel slice wn (each slice's weights loaded by both of its wavefronts).
+  constexpr int NW = 4, NT = 256 * RS, KC = 64, PC = KC / 8;
+  constexpr int TM = BM / 32 / RS, TN = 2, AL = BM * PC / NT;  // TM groups of 32 rows per wavefront
+  static_assert(AL == TM, "one A DMA per 32-row group");
+  constexpr int BQ = 8 / TM;                                 // weight loads per 32-row group (8 per stage)
   static_assert(BM == 128 || BM == 256, "tile rows");
   __shared__ __attribute__((aligned(16))) u32x4 As0[BM * PC], As1[BM * PC], As2[BM * PC], As3[BM * PC];
   __shared__ uint32_t srcT[BM * 27];
   __shared__ int ordT[BM];
-  __shared__ uint32_t gmask[TM];
+  __shared__ uint32_t gmask[BM / 32];
   __shared__ int vlist[32];
 
   const int g = blockIdx.x, per = a.grid / 8;
@@ -1155,7 +1158,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   const int tm_ = logical / a.tiles_n, tn_ = logical % a.tiles_n;
   const int row0 = tm_ * BM, co0 = tn_ * (64 * NW);
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
-  const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), wn = wv % NW, wr = wv / NW;
   const int N = a.N, Ci = a.Ci, nkc = Ci / KC;
 
   // prologue: the tile's block of the neighbour table goes to LDS by DMA; rows and 32-row masks from the same order
@@ -1172,21 +1175,21 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   __syncthreads();
   uint32_t mask = 0;
 #pragma unroll
-  for (int i = 0; i < TM; i++) mask |= gmask[i];
+  for (int i = 0; i < BM / 32; i++) mask |= gmask[i];
   const int nvv = __popc(mask), total = nvv * nkc;
   if (tid < 27 && ((mask >> tid) & 1u)) vlist[__popc(mask & ((1u << tid) - 1u))] = tid;
   uint32_t gms[TM];
 #pragma unroll
-  for (int i = 0; i < TM; i++) gms[i] = __builtin_amdgcn_readfirstlane(gmask[i]);
+  for (int i = 0; i < TM; i++) gms[i] = __builtin_amdgcn_readfirstlane(gmask[wr * TM + i]);
   __syncthreads();
 
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes), rw = make_rsrc(a.w, a.w_bytes);
-  // DMA k of this lane fills LDS unit u = (wn*AL + k)*64 + lane: row u/8, slot u%8, channel piece
+  // DMA k of this lane fills LDS unit u = (wv*AL + k)*64 + lane: row u/8, slot u%8, channel piece
   // slot ^ ((row >> 1) & 7)
   uint32_t drow[AL], dpiece[AL];
 #pragma unroll
   for (int k = 0; k < AL; k++) {
-    const int u = (wn * AL + k) * 64 + lane;
+    const int u = (wv * AL + k) * 64 + lane;
     drow[k] = u >> 3;
     dpiece[k] = (u & 7) ^ ((u >> 4) & 7);
   }
@@ -1209,7 +1212,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
     for (int k = 0; k < AL; k++) off[k] = nbr_offset(srcT[drow[k] * 27 + va], (uint32_t)(Ci * 2)) + dpiece[k] * 16;
   };
   auto dma = [&](u32x4* slot, int k, uint32_t off, int ka) __attribute__((always_inline)) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)&slot[(wn * AL + k) * 64],
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)&slot[(wv * AL + k) * 64],
                                              16, off, ka, 0, 0);
   };
   auto b_base = [&]() __attribute__((always_inline)) {
@@ -1237,7 +1240,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
     const int soff = b_base();
     u32x4 fa[2][4];
     auto read_fa = [&](u32x4 (&f)[4], int i) __attribute__((always_inline)) {
-      const int r = i * 32 + l32;
+      const int r = (wr * TM + i) * 32 + l32;
 #pragma unroll
       for (int j = 0; j < 4; j++) f[j] = cur[r * PC + ((h * 4 + j) ^ ((r >> 1) & 7))];
     };
@@ -1306,16 +1309,17 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   wait_vmcnt<0>();
   __syncthreads();
 
-  // epilogue through the (now idle) ring: one slot per wavefront
-  float* ew = (float*)(wn == 0 ? &As0[0] : wn == 1 ? &As1[0] : wn == 2 ? &As2[0] : &As3[0]);
-  static_assert(32 * 72 * 4 <= BM * PC * 16, "a wavefront's epilogue staging fits in one ring slot");
+  // epilogue through the (now idle) ring: RS wavefronts' staging areas per slot
+  const int es = wv / RS;
+  float* ew = (float*)(es == 0 ? &As0[0] : es == 1 ? &As1[0] : es == 2 ? &As2[0] : &As3[0]) + (wv % RS) * 32 * 72;
+  static_assert(RS * 32 * 72 * 4 <= BM * PC * 16, "the wavefronts' epilogue staging fits in the ring slots");
   const int co_w = co0 + wn * 64;
   float bias8[8];
 #pragma unroll
   for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[co_w + (lane & 7) * 8 + q] : 0.f;
-  const int nrows = N - row0;
+  const int nrows = N - row0 - wr * TM * 32;
   const Epi e = make_epi(a);
-  epilogue_tile<TM, TN>(acc, ew, ordT, nrows, co_w, bias8, e, a.Co, lane);
+  epilogue_tile<TM, TN>(acc, ew, ordT + wr * TM * 32, nrows, co_w, bias8, e, a.Co, lane);
 }
 
 int cu_count() {
@@ -1337,7 +1341,8 @@ void launch_wide_dma_bm(ConvArgs a) {
   a.tiles_n = a.Co / 256;
   int tiles = a.tiles_m * a.tiles_n;
   a.grid = (tiles + 7) / 8 * 8;
-  k_conv_wide_dma<F16, BM><<<a.grid, 256, 0, stream()>>>(a);
+  constexpr int RS = 1;  // RS = 2 (two wavefronts per SIMD) measured 4% slower on C3: doubled weight loads, spills
+  k_conv_wide_dma<F16, BM, RS><<<a.grid, 256 * RS, 0, stream()>>>(a);
 }
 template <bool F16>
 void launch_wide_dma(ConvArgs a) {
