@@ -1128,23 +1128,23 @@ void launch_narrow(ConvArgs a) {
   k_conv_narrow<F16, S, T, G><<<a.grid, 256, 0, stream()>>>(a);
 }
 
-// Wide-channel kernel, 256 sorted rows x 256 channels per workgroup (4 wavefronts, each all 256 rows x 64
-// channels = 8 x 2 tiles of 32x32 fp32 accumulators in AGPRs). Differences from k_conv_wide:
+// Wide-channel kernel, BM sorted rows x 256 channels per workgroup (4 wavefronts, each all BM rows x 64 channels =
+// BM/32 x 2 tiles of 32x32 fp32 accumulators). BM = 128 is the one launched: two workgroups per CU, so one
+// workgroup's prologue, barriers and epilogue overlap the other's MFMAs. Differences from k_conv_wide:
 //  * The gathered A tile goes global -> LDS directly (buffer_load ... lds, 16 bytes per lane; EMPTY neighbours
 //    read past the buffer end and land as zeros) into a 4-slot LDS ring, 3 stages ahead of the MFMAs: no
 //    registers hold gathers in flight, and gather latency hides behind three stages of MFMA work. The slots are
 //    four distinct LDS objects so the compiler can tell the DMA into one slot from the reads of another.
 //  * Ring protocol per stage s: wait (counted vmcnt) for this lane's DMA of A(s), barrier (every wavefront's
-//    part has landed and everyone is done with stage s-1), then, between the MFMA groups of stage s, refill the
-//    slot stage s-1 used with A(s+3) and load the weights of stage s+1 into the other register set.
-template <bool F16, int BM, int RS>
-__global__ void __launch_bounds__(256 * RS, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvArgs a) {
-  // RS = 1: 4 wavefronts, each all BM rows x 64 channels. RS = 2: 8 wavefronts (two per SIMD), wavefront (wr, wn)
-  // owns rows wr*BM/2 .. +BM/2 x channel slice wn (each slice's weights loaded by both of its wavefronts).
-  constexpr int NW = 4, NT = 256 * RS, KC = 64, PC = KC / 8;
-  constexpr int TM = BM / 32 / RS, TN = 2, AL = BM * PC / NT;  // TM groups of 32 rows per wavefront
+//    part has landed and everyone is done with stage s-1), then refill the slot stage s-1 used with A(s+3).
+//  * K-step-outer MFMA order: for each 16-wide K step j of the stage, the MFMAs of every 32-row group, then the
+//    weights of stage s+1 for step j go into the registers step j just released. One weight register set (not two),
+//    a stage of latency slack for every weight load, and BM/32 x 2 independent accumulator chains in flight.
+template <bool F16, int BM>
+__global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvArgs a) {
+  constexpr int NW = 4, NT = 256, KC = 64, PC = KC / 8;
+  constexpr int TM = BM / 32, TN = 2, AL = BM * PC / NT;  // TM groups of 32 rows per wavefront
   static_assert(AL == TM, "one A DMA per 32-row group");
-  constexpr int BQ = 8 / TM;                                 // weight loads per 32-row group (8 per stage)
   static_assert(BM == 128 || BM == 256, "tile rows");
   __shared__ __attribute__((aligned(16))) u32x4 As0[BM * PC], As1[BM * PC], As2[BM * PC], As3[BM * PC];
   __shared__ uint32_t srcT[BM * 27];
@@ -1158,7 +1158,7 @@ __global__ void __launch_bounds__(256 * RS, BM == 128 ? 2 : 1) k_conv_wide_dma(C
   const int tm_ = logical / a.tiles_n, tn_ = logical % a.tiles_n;
   const int row0 = tm_ * BM, co0 = tn_ * (64 * NW);
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), wn = wv % NW, wr = wv / NW;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), wn = wv;
   const int N = a.N, Ci = a.Ci, nkc = Ci / KC;
 
   // prologue: the tile's block of the neighbour table goes to LDS by DMA; rows and 32-row masks from the same order
@@ -1180,7 +1180,7 @@ __global__ void __launch_bounds__(256 * RS, BM == 128 ? 2 : 1) k_conv_wide_dma(C
   if (tid < 27 && ((mask >> tid) & 1u)) vlist[__popc(mask & ((1u << tid) - 1u))] = tid;
   uint32_t gms[TM];
 #pragma unroll
-  for (int i = 0; i < TM; i++) gms[i] = __builtin_amdgcn_readfirstlane(gmask[wr * TM + i]);
+  for (int i = 0; i < TM; i++) gms[i] = __builtin_amdgcn_readfirstlane(gmask[i]);
   __syncthreads();
 
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes), rw = make_rsrc(a.w, a.w_bytes);
@@ -1229,49 +1229,52 @@ __global__ void __launch_bounds__(256 * RS, BM == 128 ? 2 : 1) k_conv_wide_dma(C
 #pragma unroll
     for (int t = 0; t < TN; t++) acc[i][t] = f32x16{};
 
-  // one K stage: MFMAs from slot `cur` and weights rbC; DMA A(s+3) into `fill`; weights of s+1 into rbN
-  auto stage = [&](const u32x4* cur, u32x4* fill, const u32x4 (&rbC)[TN][4], u32x4 (&rbN)[TN][4])
-      __attribute__((always_inline)) {
+  // one K stage: MFMAs from slot `cur` and the weights in rb (stage s); DMA A(s+3) into `fill`; rb refilled with
+  // the weights of stage s+1, K step by K step
+  auto stage = [&](const u32x4* cur, u32x4* fill, u32x4 (&rb)[TN][4]) __attribute__((always_inline)) {
     const uint32_t vbit = 1u << __builtin_amdgcn_readfirstlane(vlist[cvi]);
     next(cvi, ckc);
     uint32_t off[AL];
     int ka;
     a_offsets(off, ka);
     const int soff = b_base();
-    u32x4 fa[2][4];
-    auto read_fa = [&](u32x4 (&f)[4], int i) __attribute__((always_inline)) {
-      const int r = (wr * TM + i) * 32 + l32;
+    u32x4 fa[2][TM];
+    auto read_j = [&](u32x4 (&f)[TM], int j) __attribute__((always_inline)) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) f[j] = cur[r * PC + ((h * 4 + j) ^ ((r >> 1) & 7))];
-    };
-    read_fa(fa[0], 0);
-#pragma unroll
-    for (int i = 0; i < TM; i++) {
-      dma(fill, i, off[i], ka);
-#pragma unroll
-      for (int q = i * BQ; q < (i + 1) * BQ; q++)
-        rbN[q / 4][q % 4] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + q * 1024, soff, 0);
-      if (i + 1 < TM) read_fa(fa[(i + 1) & 1], i + 1);
-      if (gms[i] & vbit) {
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-          for (int t = 0; t < TN; t++) acc[i][t] = mfma32<F16>(fa[i & 1][j], rbC[t][j], acc[i][t]);
+      for (int i = 0; i < TM; i++) {
+        const int r = i * 32 + l32;
+        f[i] = cur[r * PC + ((h * 4 + j) ^ ((r >> 1) & 7))];
       }
+    };
+    read_j(fa[0], 0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+      for (int k = (j * AL) / 4; k < ((j + 1) * AL) / 4; k++) dma(fill, k, off[k], ka);
+      if (j + 1 < 4) read_j(fa[(j + 1) & 1], j + 1);
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        if (gms[i] & vbit) {
+#pragma unroll
+          for (int t = 0; t < TN; t++) acc[i][t] = mfma32<F16>(fa[j & 1][i], rb[t][j], acc[i][t]);
+        }
+#pragma unroll
+      for (int t = 0; t < TN; t++)
+        rb[t][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + (t * 4 + j) * 1024, soff, 0);
     }
   };
   // loads issued after this lane's last DMA of A(s) when stage s starts: prologue DMAs and B(0) for s < 3,
-  // then (in steady state) the last group's weight loads of stage s-3 plus two full stages of AL + 8
+  // then (in steady state) the last K step's TN weight loads of stage s-3 plus two full stages of AL + 8
   constexpr int SL = AL + 8;
   auto wait_a = [&](int s) __attribute__((always_inline)) {
     if (s == 0) wait_vmcnt<2 * AL + 8>();
     else if (s == 1) wait_vmcnt<AL + 8 + SL>();
     else if (s == 2) wait_vmcnt<8 + 2 * SL>();
-    else wait_vmcnt<BQ + 2 * SL>();
+    else wait_vmcnt<TN + 2 * SL>();
   };
 
   if (total > 0) {
-    u32x4 rb0[TN][4], rb1[TN][4];
+    u32x4 rb[TN][4];
     {
       uint32_t off[AL];
       int ka;
@@ -1286,68 +1289,52 @@ __global__ void __launch_bounds__(256 * RS, BM == 128 ? 2 : 1) k_conv_wide_dma(C
       for (int k = 0; k < AL; k++) dma(As2, k, off[k], ka);
       const int soff = b_base();
 #pragma unroll
-      for (int q = 0; q < 8; q++) rb0[q / 4][q % 4] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + q * 1024, soff, 0);
+      for (int q = 0; q < 8; q++) rb[q / 4][q % 4] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + q * 1024, soff, 0);
     }
     for (int s = 0; s < total; s += 4) {
       wait_a(s);
       wg_barrier();
-      stage(As0, As3, rb0, rb1);
+      stage(As0, As3, rb);
       if (s + 1 >= total) break;
       wait_a(s + 1);
       wg_barrier();
-      stage(As1, As0, rb1, rb0);
+      stage(As1, As0, rb);
       if (s + 2 >= total) break;
       wait_a(s + 2);
       wg_barrier();
-      stage(As2, As1, rb0, rb1);
+      stage(As2, As1, rb);
       if (s + 3 >= total) break;
       wait_a(s + 3);
       wg_barrier();
-      stage(As3, As2, rb1, rb0);
+      stage(As3, As2, rb);
     }
   }
   wait_vmcnt<0>();
   __syncthreads();
 
-  // epilogue through the (now idle) ring: RS wavefronts' staging areas per slot
-  const int es = wv / RS;
-  float* ew = (float*)(es == 0 ? &As0[0] : es == 1 ? &As1[0] : es == 2 ? &As2[0] : &As3[0]) + (wv % RS) * 32 * 72;
-  static_assert(RS * 32 * 72 * 4 <= BM * PC * 16, "the wavefronts' epilogue staging fits in the ring slots");
+  // epilogue through the (now idle) ring: one slot per wavefront
+  float* ew = (float*)(wv == 0 ? &As0[0] : wv == 1 ? &As1[0] : wv == 2 ? &As2[0] : &As3[0]);
+  static_assert(32 * 72 * 4 <= BM * PC * 16, "a wavefront's epilogue staging fits in a ring slot");
   const int co_w = co0 + wn * 64;
   float bias8[8];
 #pragma unroll
   for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[co_w + (lane & 7) * 8 + q] : 0.f;
-  const int nrows = N - row0 - wr * TM * 32;
+  const int nrows = N - row0;
   const Epi e = make_epi(a);
-  epilogue_tile<TM, TN>(acc, ew, ordT + wr * TM * 32, nrows, co_w, bias8, e, a.Co, lane);
+  epilogue_tile<TM, TN>(acc, ew, ordT, nrows, co_w, bias8, e, a.Co, lane);
 }
 
-int cu_count() {
-  static int n = 0;
-  if (!n) {
-    int dev = 0;
-    CK(hipGetDevice(&dev));
-    CK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
-  }
-  return n;
-}
-
-// 256-row tiles (one workgroup per CU) unless that leaves fewer than two tiles per CU: then 128-row tiles, two
-// workgroups per CU, so a small-N wide layer (C2: 297 tiles of 256 rows for 256 CUs) does not spend its second
-// round on a few tiles.
-template <bool F16, int BM>
-void launch_wide_dma_bm(ConvArgs a) {
-  a.tiles_m = cdiv(a.N, BM);
-  a.tiles_n = a.Co / 256;
-  int tiles = a.tiles_m * a.tiles_n;
-  a.grid = (tiles + 7) / 8 * 8;
-  constexpr int RS = 1;  // RS = 2 (two wavefronts per SIMD) measured 4% slower on C3: doubled weight loads, spills
-  k_conv_wide_dma<F16, BM, RS><<<a.grid, 256 * RS, 0, stream()>>>(a);
-}
+// 128-row tiles, two workgroups per CU. Measured on C3 (1526 tiles of 256 rows): 256-row tiles with one workgroup
+// per CU were 6% slower (prologue, barriers and epilogue exposed; 2x fewer weight loads per flop did not make up
+// for it), as were 8 wavefronts of 128 rows x 64 channels on a 256-row tile (3% slower: weights loaded twice).
 template <bool F16>
 void launch_wide_dma(ConvArgs a) {
-  if ((i64)cdiv(a.N, 256) * (a.Co / 256) < 2 * (i64)cu_count()) launch_wide_dma_bm<F16, 128>(a);
-  else launch_wide_dma_bm<F16, 256>(a);
+  constexpr int BM = 128;
+  a.tiles_m = cdiv(a.N, BM);
+  a.tiles_n = a.Co / 256;
+  const int tiles = a.tiles_m * a.tiles_n;
+  a.grid = (tiles + 7) / 8 * 8;
+  k_conv_wide_dma<F16, BM><<<a.grid, 256, 0, stream()>>>(a);
 }
 
 template <bool F16, int NW, int BM>
