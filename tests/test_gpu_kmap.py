@@ -143,6 +143,33 @@ def test_lookup(gpu, name):
     assert sp.lookup(empty, torch.from_numpy(q[:9]).to(gpu)).cpu().tolist() == [-1] * 9
 
 
+@pytest.mark.parametrize("permute", [False, True])
+def test_lookup_large(gpu, permute):
+    """C4-size kept hash (a table of >= 2^22 slots, sized on the device from the brick-key runs of the input): every
+    voxel finds its own row, and +x / +y shifted queries of a sample match a sorted-key search. Permuted input has
+    about one run per voxel, so the table keeps its full size."""
+    c = coords("c4")
+    if permute:
+        c = c[np.random.default_rng(5).permutation(len(c))]
+    print(f"lookup_large permute={permute} n={len(c)}", flush=True)
+    R = 1024
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu), R, R, R, keep_hash=True)
+    got = sp.lookup(cache, torch.from_numpy(c).to(gpu)).cpu().numpy()
+    np.testing.assert_array_equal(got, np.arange(len(c)))
+    key = lambda a: ((a[:, 0].astype(np.int64) * R + a[:, 1]) * R + a[:, 2]) * R + a[:, 3]
+    k = key(c)
+    srt = np.argsort(k)
+    ks = k[srt]
+    samp = c[np.random.default_rng(6).choice(len(c), 200000, replace=False)]
+    for d in ([0, 1, 0, 0], [0, 0, 1, 0], [0, 0, 0, -1]):
+        q = samp + np.array(d, np.int32)
+        inside = ((q[:, 1:] >= 0) & (q[:, 1:] < R)).all(1)
+        qk = key(np.where(inside[:, None], q, 0))
+        pos = np.minimum(np.searchsorted(ks, qk), len(ks) - 1)
+        want = np.where(inside & (ks[pos] == qk), srt[pos], -1)
+        np.testing.assert_array_equal(sp.lookup(cache, torch.from_numpy(q).to(gpu)).cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("name,R", [("c1", 32), ("c1", 20)])
 def test_fdg_quads(gpu, name, R):
     """Quads from the kernel map equal the reference rule evaluated with a dictionary hash (ok flags everywhere,

@@ -54,7 +54,8 @@ struct SpConvCache {
   // The brick hash, kept when built with keep_hash (for coordinate lookups by other consumers): slot table,
   // brick records, slot mask and the grid bounds.
   Tensor htable, hbricks;
-  uint32_t hmask = 0;
+  uint32_t hmask = 0;  // the table's slot mask, or (when hmaskd is set) its allocated capacity - 1
+  Tensor hmaskd;       // device u32 mask of large tables (sized on the device from the brick count)
   int W = 0, H = 0, D = 0;
 };
 // coords int32 [N,4] (b,x,y,z); keep_hash keeps the brick hash in the cache (~32-128 B + 256 B per voxel) so that
