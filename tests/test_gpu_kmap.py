@@ -96,6 +96,16 @@ def test_kmap_random_permutation(gpu):
     check_map(c, gpu)
 
 
+@pytest.mark.parametrize("n", [1048576, 1048577])
+def test_kmap_sort_paths(gpu, n):
+    """The stable sort switches from the tile look-back form (at most 256 tiles of 4096 keys) to count/scan/scatter
+    passes above it: both sides of the switch, on a permuted prefix of the c4 shell (ties in non-Morton order)."""
+    c = coords("c4")[:n].copy()
+    c = c[np.random.default_rng(1).permutation(n)]
+    print(f"sort path n={n}", flush=True)
+    check_map(c, gpu, B1s=(128,))
+
+
 @pytest.mark.parametrize("name", ["c1", "c5"])
 def test_subdivide(gpu, name):
     par = coords(name)
