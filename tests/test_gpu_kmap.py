@@ -96,9 +96,9 @@ def test_kmap_random_permutation(gpu):
     check_map(c, gpu)
 
 
-@pytest.mark.parametrize("n", [1048576, 1048577])
+@pytest.mark.parametrize("n", [524288, 524289])
 def test_kmap_sort_paths(gpu, n):
-    """The stable sort switches from the tile look-back form (at most 256 tiles of 4096 keys) to count/scan/scatter
+    """The stable sort switches from the tile look-back form (at most 256 tiles of 2048 keys) to count/scan/scatter
     passes above it: both sides of the switch, on a permuted prefix of the c4 shell (ties in non-Morton order)."""
     c = coords("c4")[:n].copy()
     c = c[np.random.default_rng(1).permutation(n)]

@@ -2,26 +2,29 @@
 // permutation (src/spconv.cu:47-52: cub::DeviceRadixSort::SortPairs(bin -> iota), stable, bits 0..32; bin < 2^27
 // so bits 27..31 are all zero and sorting 27 bits gives the same order).
 //
-// Up to 256 tiles of 4096 keys (~1M keys, C3 and smaller): five launches for three passes (a zero fill, one
+// Up to 256 tiles of 2048 keys (512k keys, C3 and smaller): five launches for three passes (a zero fill, one
 // histogram kernel for every pass's digit, one kernel per pass):
 //   hist    : global digit histograms of all passes at once (LDS counts per tile, then global adds)
 //   pass    : a workgroup takes the next tile ticket (an atomic counter, so tiles start in ticket order) and ranks
-//             its keys: each wavefront ranks its 16 chunks in order; within a chunk, lanes holding the same digit
-//             find each other with 9 ballots (one per digit bit) and take rank = popcount(peers below me); wavefront
-//             counts are prefixed across the 4 wavefronts. Per digit the tile publishes its count, looks back over
-//             the tiles before it, 8 per round (each publishes its count at once, then its inclusive prefix, so the
-//             look-back stops at the first inclusive prefix it meets) and publishes its own inclusive prefix. Destination =
-//             digit start (exclusive scan of the histogram) + tiles before + wavefronts before + rank, so every key
-//             keeps its input order among equal digits.
+//             its keys: each wavefront ranks its 8 chunks of 64 keys in order; within a chunk, lanes holding the
+//             same digit find each other with 9 ballots (one per digit bit) and take rank = popcount(peers below
+//             me); wavefront counts are prefixed across the 4 wavefronts. Per digit the tile publishes its count,
+//             looks back over the tiles before it, 16 per round (each publishes its count at once, then its
+//             inclusive prefix, so the look-back stops at the first inclusive prefix it meets) and publishes its
+//             own inclusive prefix. Destination = digit start (exclusive scan of the histogram) + tiles before +
+//             wavefronts before + rank, so every key keeps its input order among equal digits.
 // A look-back only waits on tiles with a smaller ticket, which are already running and publish their counts without
 // waiting; the wait is bounded all the same (a tile that never published would read as empty: wrong order, no hang).
-// Beyond 256 tiles the chain of published prefixes gets long (C4, 643 tiles: 0.46 -> 0.49 ms build), so larger
-// sorts run three kernels per pass over the same ranking: per-tile digit counts (digit-major), an exclusive scan of
-// them, and the scatter with those starts.
+// Beyond 256 tiles the chain of published prefixes gets long (C4: 0.46 -> 0.49 ms build), so larger sorts run
+// three kernels per pass over the same ranking (tiles of 4096 keys): per-tile digit counts (digit-major), an
+// exclusive scan of them, and the scatter with those starts.
 #include "scan.h"
 
 namespace {
-constexpr int RBITS = 9, NBUK = 1 << RBITS, RT = 256, RCH = 16, RTILE = RT * RCH, MAXP = 4, LB = 8;
+constexpr int RBITS = 9, NBUK = 1 << RBITS, RT = 256, MAXP = 4;
+// look-back form: tiles of RT x RCH_LB keys (C2's 25k keys: 13 tiles, 0.085 -> 0.068 ms build against 4096-key
+// tiles), LB tiles read per look-back round; count/scan/scatter form: tiles of RT x RCH_CS keys
+constexpr int RCH_LB = 8, RTILE_LB = RT * RCH_LB, LB = 16, RCH_CS = 16, RTILE_CS = RT * RCH_CS;
 constexpr uint64_t ST_AGG = 1ull << 32, ST_INC = 2ull << 32;
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr int kLookbackTiles = 256;
@@ -29,6 +32,7 @@ constexpr int kLookbackTiles = 256;
 // Ranks a wavefront's RCH chunks of 64 keys (rows seg .. seg + RCH*64) by the digit at `shift`, in input order: lanes
 // holding the same digit find each other with RBITS ballots and take rank = popcount(peers below me) plus the
 // wavefront's running count for that digit (cw, in LDS, zeroed by the caller), which the lowest peer advances.
+template <int RCH>
 __device__ __forceinline__ void rank_chunks(const uint32_t* __restrict__ kin, const int32_t* __restrict__ vin, i64 n,
                                             int shift, i64 seg, int lane, uint32_t* cw, uint32_t (&key)[RCH],
                                             int32_t (&val)[RCH], uint32_t (&rank)[RCH]) {
@@ -62,9 +66,9 @@ __global__ void __launch_bounds__(RT) k_rs_hist(const uint32_t* __restrict__ key
   __shared__ uint32_t cnt[MAXP][NBUK];
   for (int d = threadIdx.x; d < MAXP * NBUK; d += RT) (&cnt[0][0])[d] = 0;
   __syncthreads();
-  const i64 base = (i64)blockIdx.x * RTILE;
+  const i64 base = (i64)blockIdx.x * RTILE_LB;
 #pragma unroll 4
-  for (int j = 0; j < RCH; j++) {
+  for (int j = 0; j < RCH_LB; j++) {
     const i64 i = base + j * RT + threadIdx.x;
     if (i < n) {
       const uint32_t k = keys[i];
@@ -107,10 +111,10 @@ __global__ void __launch_bounds__(RT) k_rs_pass(const uint32_t* __restrict__ kin
   start[2 * threadIdx.x + 1] = ex + h0;
   const int tile = tile_s;
 
-  const i64 seg = (i64)tile * RTILE + (i64)wv * (RCH * 64);
-  uint32_t key[RCH], rank[RCH];
-  int32_t val[RCH];
-  rank_chunks(kin, vin, n, shift, seg, lane, cnt[wv], key, val, rank);
+  const i64 seg = (i64)tile * RTILE_LB + (i64)wv * (RCH_LB * 64);
+  uint32_t key[RCH_LB], rank[RCH_LB];
+  int32_t val[RCH_LB];
+  rank_chunks<RCH_LB>(kin, vin, n, shift, seg, lane, cnt[wv], key, val, rank);
   __syncthreads();
   for (int d = threadIdx.x; d < NBUK; d += RT) {
     uint32_t run = 0;
@@ -132,8 +136,9 @@ __global__ void __launch_bounds__(RT) k_rs_pass(const uint32_t* __restrict__ kin
         uint64_t w[LB];
 #pragma unroll
         for (int k = 0; k < LB; k++)
-          w[k] = j - k >= 0 ? __hip_atomic_load(st + (i64)(j - k) * NBUK + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                            : ST_INC;
+          w[k] = j - k >= 0
+                     ? __hip_atomic_load(st + (i64)(j - k) * NBUK + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                     : ST_INC;
         int k = 0;
         bool done = false;
         for (; k < LB; k++) {
@@ -155,7 +160,7 @@ __global__ void __launch_bounds__(RT) k_rs_pass(const uint32_t* __restrict__ kin
   }
   __syncthreads();
 #pragma unroll
-  for (int c = 0; c < RCH; c++) {
+  for (int c = 0; c < RCH_LB; c++) {
     const i64 i = seg + c * 64 + lane;
     if (i < n) {
       const uint32_t d = (key[c] >> shift) & (NBUK - 1);
@@ -170,9 +175,9 @@ __global__ void __launch_bounds__(RT) k_rs_count(const uint32_t* __restrict__ ke
   __shared__ uint32_t cnt[NBUK];
   for (int d = threadIdx.x; d < NBUK; d += RT) cnt[d] = 0;
   __syncthreads();
-  i64 base = (i64)blockIdx.x * RTILE;
+  i64 base = (i64)blockIdx.x * RTILE_CS;
 #pragma unroll 4
-  for (int j = 0; j < RCH; j++) {
+  for (int j = 0; j < RCH_CS; j++) {
     i64 i = base + j * RT + threadIdx.x;
     if (i < n) atomicAdd(&cnt[(keys[i] >> shift) & (NBUK - 1)], 1u);
   }
@@ -188,10 +193,10 @@ __global__ void __launch_bounds__(RT) k_rs_scatter(const uint32_t* __restrict__ 
   for (int d = threadIdx.x; d < NBUK; d += RT)
     for (int w = 0; w < RT / 64; w++) cnt[w][d] = 0;
   __syncthreads();
-  const i64 seg = (i64)blockIdx.x * RTILE + (i64)wv * (RCH * 64);
-  uint32_t key[RCH], rank[RCH];
-  int32_t val[RCH];
-  rank_chunks(kin, vin, n, shift, seg, lane, cnt[wv], key, val, rank);
+  const i64 seg = (i64)blockIdx.x * RTILE_CS + (i64)wv * (RCH_CS * 64);
+  uint32_t key[RCH_CS], rank[RCH_CS];
+  int32_t val[RCH_CS];
+  rank_chunks<RCH_CS>(kin, vin, n, shift, seg, lane, cnt[wv], key, val, rank);
   __syncthreads();
   for (int d = threadIdx.x; d < NBUK; d += RT) {
     uint32_t run = start[(i64)d * ntiles + blockIdx.x];
@@ -204,7 +209,7 @@ __global__ void __launch_bounds__(RT) k_rs_scatter(const uint32_t* __restrict__ 
   }
   __syncthreads();
 #pragma unroll
-  for (int c = 0; c < RCH; c++) {
+  for (int c = 0; c < RCH_CS; c++) {
     i64 i = seg + c * 64 + lane;
     if (i < n) {
       uint32_t d = (key[c] >> shift) & (NBUK - 1);
@@ -221,7 +226,6 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
   REQ(n < (1ll << 31), "sort size %lld", (long long)n);
   REQ(bits >= 1 && bits <= 32, "key bits %d", bits);
   const int passes = (bits + RBITS - 1) / RBITS;
-  const int ntiles = cdiv(n, RTILE);
   hipStream_t s = stream();
   Tensor kb0 = empty({n}, I32), kb1 = empty({n}, I32), vb0 = empty({n}, I32), vb1 = empty({n}, I32);
   // ping-pong buffers; the last pass writes its values straight into vals_out
@@ -231,7 +235,8 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
     kout = (p & 1) ? kb1.ptr<uint32_t>() : kb0.ptr<uint32_t>();
     vout = p + 1 == passes ? vals_out : ((p & 1) ? vb1.ptr<int32_t>() : vb0.ptr<int32_t>());
   };
-  if (ntiles <= kLookbackTiles) {
+  if (cdiv(n, RTILE_LB) <= kLookbackTiles) {
+    const int ntiles = cdiv(n, RTILE_LB);
     // one zeroed block: histograms [passes][NBUK], tickets (64 words), look-back words [passes][ntiles][NBUK]
     const i64 hwords = (i64)passes * NBUK, twords = 64, swords = (i64)passes * ntiles * NBUK * 2;
     const i64 zw = hwords + twords + swords;
@@ -251,6 +256,7 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
       vin = vout;
     }
   } else {
+    const int ntiles = cdiv(n, RTILE_CS);
     const i64 nh = (i64)NBUK * ntiles;
     Tensor hist = empty({nh}, I32);
     for (int p = 0; p < passes; p++) {
