@@ -166,30 +166,90 @@ __global__ void __launch_bounds__(256) k_neighbors_brick(const int4* __restrict_
   const int W4 = (W + 3) >> 2, H4 = (H + 3) >> 2, D4 = (D + 3) >> 2;
   // the brick across a face in one axis: -1 / +1 when the coordinate is on the brick's low / high face, else none
   auto side = [](int x) __attribute__((always_inline)) { return (x & 3) == 0 ? -1 : ((x & 3) == 3 ? 1 : 0); };
-  for (int task = threadIdx.x; task < nv * 8; task += 256) {
-    const int li = task >> 3, cb = task & 7;
-    const int4 q = cq[li];
+  // candidate bricks: 8 tasks per voxel, 4 per thread, probed together (first probes issued at once; linear
+  // probing at load <= 0.5 resolves in ~1.5 rounds)
+  constexpr int NT = NV * 8 / 256;
+  uint64_t key[NT];
+  uint32_t slot[NT], ids[NT];
+  bool pend[NT];
+#pragma unroll
+  for (int u = 0; u < NT; u++) {
+    const int task = threadIdx.x + 256 * u, li = task >> 3, cb = task & 7;
+    const int4 q = cq[li < nv ? li : 0];
     const int sx = (cb & 1) ? side(q.y) : 0, sy = (cb & 2) ? side(q.z) : 0, sz = (cb & 4) ? side(q.w) : 0;
     const int bx = (q.y >> 2) + sx, by = (q.z >> 2) + sy, bz = (q.w >> 2) + sz;
-    uint32_t id = EMPTY;
     const bool needed = ((cb & 1) == 0 || sx != 0) && ((cb & 2) == 0 || sy != 0) && ((cb & 4) == 0 || sz != 0);
-    if (needed && bx >= 0 && bx < W4 && by >= 0 && by < H4 && bz >= 0 && bz < D4)
-      id = brick_find(t, (((uint64_t)(uint32_t)q.x * W4 + bx) * H4 + by) * D4 + bz, mask);
-    bid[li][cb] = id;
+    pend[u] = li < nv && needed && bx >= 0 && bx < W4 && by >= 0 && by < H4 && bz >= 0 && bz < D4;
+    key[u] = (((uint64_t)(uint32_t)q.x * W4 + bx) * H4 + by) * D4 + bz;
+    slot[u] = pend[u] ? brick_home(key[u], mask) : 0u;
+    ids[u] = EMPTY;
+  }
+  for (;;) {
+    bool any = false;
+#pragma unroll
+    for (int u = 0; u < NT; u++) any |= pend[u];
+    if (!any) break;
+    ulonglong2 e[NT];
+#pragma unroll
+    for (int u = 0; u < NT; u++) e[u] = t[slot[u]];  // slot 0 (a valid entry) for finished tasks
+#pragma unroll
+    for (int u = 0; u < NT; u++) {
+      if (!pend[u]) continue;
+      if (e[u].x == key[u]) {
+        ids[u] = (uint32_t)e[u].y;
+        pend[u] = false;
+      } else if (e[u].x == HEMPTY) {
+        pend[u] = false;
+      } else {
+        slot[u] = (slot[u] + 1) & mask;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NT; u++) {
+    const int task = threadIdx.x + 256 * u;
+    (&bid[0][0])[task] = ids[u];
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < nv * 27; p += 256) {
+  // (voxel, offset) pairs p = threadIdx.x + 256 k: record addresses first, then every record load, then the
+  // stores and the mask bits. Offset v = 9 dx' + 3 dy' + dz' with v / 9 = (57 v) >> 9 and v / 3 = (11 v) >> 5
+  // for v < 27.
+  constexpr int NPR = (NV * 27 + 255) / 256;
+  i64 addr[NPR];
+  bool hit[NPR];
+#pragma unroll
+  for (int k = 0; k < NPR; k++) {
+    const int p = threadIdx.x + 256 * k;
     const int li = p / 27, v = p - li * 27;
-    const int4 q = cq[li];
-    const int x = q.y + v / 9 - 1, y = q.z + v / 3 % 3 - 1, z = q.w + v % 3 - 1;
-    uint32_t r = EMPTY;
-    if (x >= 0 && x < W && y >= 0 && y < H && z >= 0 && z < D) {
-      const int cb = ((x >> 2) != (q.y >> 2) ? 1 : 0) | ((y >> 2) != (q.z >> 2) ? 2 : 0) | ((z >> 2) != (q.w >> 2) ? 4 : 0);
-      const uint32_t id = bid[li][cb];
-      if (id != EMPTY) r = bricks[(i64)id * 64 + brick_local(x, y, z)];
+    const int4 q = cq[li < nv ? li : 0];
+    const int v9 = (v * 57) >> 9, v3 = (v * 11) >> 5;
+    const int x = q.y + v9 - 1, y = q.z + v3 - 3 * v9 - 1, z = q.w + v - 3 * v3 - 1;
+    const bool inb = p < nv * 27 && x >= 0 && x < W && y >= 0 && y < H && z >= 0 && z < D;
+    const int cb = ((x >> 2) != (q.y >> 2) ? 1 : 0) | ((y >> 2) != (q.z >> 2) ? 2 : 0) | ((z >> 2) != (q.w >> 2) ? 4 : 0);
+    const uint32_t id = inb ? bid[li][cb] : EMPTY;
+    hit[k] = id != EMPTY;
+    addr[k] = hit[k] ? (i64)id * 64 + brick_local(x, y, z) : 0;
+  }
+  uint32_t r[NPR];
+#pragma unroll
+  for (int k = 0; k < NPR; k++) r[k] = bricks[addr[k]];  // entry 0 (a valid address) for misses
+  // mask bits: a voxel's offsets are consecutive lanes, so the first lane of each voxel's run in a wavefront ORs
+  // the run's ballot bits (shifted to the run's first offset) into the voxel's mask: a few LDS atomics per
+  // wavefront instead of one per found neighbour (27 lanes on one address serialise)
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < NPR; k++) {
+    const int p = threadIdx.x + 256 * k;
+    const bool live = p < nv * 27;
+    const uint32_t rv = hit[k] ? r[k] : EMPTY;
+    if (live) nbr[v0 * 27 + p] = rv;
+    const uint64_t found = __ballot(live && rv != EMPTY);
+    const int li = p / 27, v = p - li * 27;
+    if (live && (v == 0 || lane == 0)) {
+      const int len = min(27 - v, 64 - lane);
+      const uint32_t bits = (uint32_t)((found >> lane) & ((1ull << len) - 1ull)) << v;
+      if (bits) atomicOr(&gm[li], bits);
     }
-    nbr[v0 * 27 + p] = r;
-    if (r != EMPTY) atomicOr(&gm[li], 1u << v);
   }
   __syncthreads();
   if ((int)threadIdx.x < nv) {
