@@ -619,22 +619,33 @@ __global__ void __launch_bounds__(B) k_halo_build(const uint32_t* __restrict__ n
                                                   int32_t* __restrict__ overflow) {
   constexpr int NWV = B / 64, SPT = kHaloSlots / B;  // wavefronts, slots per thread
   static_assert(B % 64 == 0 && B <= 256 && UM < 65535 && 2 * UM <= kHaloSlots, "halo tile shape");
+  // B-row windows (SpConvCache::window_order(log2 B)): tile t holds exactly the rows t*B .. t*B + B
   __shared__ uint32_t keys[kHaloSlots];
   __shared__ int pos[kHaloSlots];
+  __shared__ __attribute__((aligned(16))) uint32_t nbL[B * 27];
   __shared__ int wsum[NWV];
   __shared__ int bad;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const i64 t = blockIdx.x, p = t * B + tid;  // position in the tile order; its row is order[p]
   const i64 r = p < n ? order[p] : n;
+  // the tile order permutes rows inside B-row windows, so the tile's neighbour rows are the contiguous block
+  // nbr[t*B .. t*B + B): copied to LDS with 16-byte loads (27 strided 4-byte loads per thread touched 64 lines each)
+  const i64 r0 = t * B;
+  const int nw = (int)min<i64>(B, n - r0) * 27;
+  const uint4* src4 = (const uint4*)(nbr + r0 * 27);  // r0 * 108 bytes: 16-byte aligned (B % 4 == 0)
+  for (int i = tid; i < nw / 4; i += B) ((uint4*)nbL)[i] = src4[i];
+  for (int i = nw / 4 * 4 + tid; i < nw; i += B) nbL[i] = nbr[r0 * 27 + i];
   for (int i = tid; i < kHaloSlots; i += B) keys[i] = EMPTY;
   if (tid == 0) bad = 0;
   __syncthreads();
+  const bool inwin = r >= r0 && r < r0 + B;  // always, for a window order; otherwise the tile is flagged
+  if (r < n && !inwin) bad = 1;
   uint32_t nb[27];
   int16_t sl[27];
   uint32_t mask = 0;
 #pragma unroll
   for (int v = 0; v < 27; v++) {
-    nb[v] = r < n ? nbr[r * 27 + v] : EMPTY;
+    nb[v] = r < n && inwin ? nbL[(r - r0) * 27 + v] : EMPTY;
     sl[v] = -1;
     if (nb[v] == EMPTY) continue;
     mask |= 1u << v;
