@@ -9,9 +9,9 @@
 // with a 64-bit compare-and-swap; the slot hash is MurmurHash3's 32-bit finalizer (fmix32, Austin Appleby, public
 // domain) of the folded key.
 //
-// Neighbour map: one thread per (voxel, offset) pair, 128 voxels x 27 offsets per 256-thread workgroup, so the
-// [N,27] output is written as one contiguous, fully coalesced range per workgroup. The 27-bit mask is assembled
-// with LDS atomic OR, then decoded (gray -> binary prefix xor) by one thread per voxel.
+// Neighbour map: one thread per voxel; its candidate bricks are probed once and kept in registers, its 27 rows
+// read from the brick records, its mask assembled in registers and decoded (gray -> binary prefix xor), and the
+// [N,27] rows of a 256-voxel workgroup written through LDS as one contiguous, fully coalesced range.
 #include "scan.h"
 #include "spconv.h"
 
@@ -26,8 +26,6 @@ __global__ void k_table_clear(ulonglong2* __restrict__ t, uint32_t mask, const u
   for (i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x; i < cap; i += (i64)gridDim.x * blockDim.x)
     t[i] = make_ulonglong2(HEMPTY, HEMPTY);
 }
-
-constexpr int NV = 128;  // voxels per workgroup in the neighbour kernel (64: 2% slower on C4)
 
 // ------------------------------------------------------------------------------------------ brick table
 // Exact lookup structure for the neighbour query (only its answers are observable: nbr rows are bit-exact whatever
@@ -141,126 +139,107 @@ __global__ void __launch_bounds__(256) k_brick_fill(const int4* __restrict__ c, 
   bricks[(i64)id * 64 + brick_local(q.y, q.z, q.w)] = (uint32_t)i;
 }
 
-// 128 voxels x 27 offsets per workgroup. First each voxel's candidate bricks are looked up once: per axis its own
-// brick and, when it sits on the brick's low or high face, the brick across that face (at most 8, 3.4 on average:
-// one table probe each, not one per offset). Then one thread per (voxel, offset) pair reads the neighbour's row
-// from its brick's record, so the [N,27] output is one contiguous, fully coalesced range per workgroup; the 27-bit
-// mask is assembled with LDS atomic OR and decoded (gray -> binary prefix xor) by one thread per voxel.
-__global__ void __launch_bounds__(256) k_neighbors_brick(const int4* __restrict__ c, i64 n, int W, int H, int D,
-                                                         const ulonglong2* __restrict__ t,
-                                                         uint32_t mask0, const uint32_t* __restrict__ maskp,
-                                                         const uint32_t* __restrict__ bricks,
-                                                         uint32_t* __restrict__ nbr, int32_t* __restrict__ gray,
-                                                         uint32_t* __restrict__ bin) {
+// One thread per voxel, 256 voxels per workgroup. The thread probes its own voxel's candidate bricks (own brick,
+// and across each face the voxel sits on: 1-8, 3.4 on average), keeps the ids in registers, and then reads the
+// 27 neighbour rows from the brick records with every per-offset quantity a compile-time constant except three
+// face flags per axis; the mask is assembled in registers. The rows go through LDS so the [N,27] output is one
+// contiguous, fully coalesced range per workgroup. Measured against one thread per (voxel, offset) pair with the
+// candidate ids shared through LDS and the mask assembled by wavefront ballots: C4 220 -> 162 us, C3 32 -> 23 us
+// (per-pair index arithmetic, LDS round trips and barriers were most of that kernel's time).
+constexpr int NVV = 256;
+__global__ void __launch_bounds__(NVV) k_neighbors_vox(const int4* __restrict__ c, i64 n, int W, int H, int D,
+                                                       const ulonglong2* __restrict__ t,
+                                                       uint32_t mask0, const uint32_t* __restrict__ maskp,
+                                                       const uint32_t* __restrict__ bricks,
+                                                       uint32_t* __restrict__ nbr, int32_t* __restrict__ gray,
+                                                       uint32_t* __restrict__ bin) {
+  __shared__ uint32_t rows[NVV * 27];
   const uint32_t mask = maskp ? *maskp : mask0;
-  __shared__ int4 cq[NV];
-  __shared__ uint32_t gm[NV];
-  __shared__ uint32_t bid[NV][8];  // candidate brick ids: bit 0/1/2 = the x/y/z brick across the voxel's face
-  const i64 v0 = (i64)blockIdx.x * NV;
-  const int nv = (int)min<i64>(NV, n - v0);
-  if (threadIdx.x < NV) {
-    gm[threadIdx.x] = 0;
-    if ((int)threadIdx.x < nv) cq[threadIdx.x] = c[v0 + threadIdx.x];
-  }
-  __syncthreads();
+  const i64 v0 = (i64)blockIdx.x * NVV;
+  const int nv = (int)min<i64>(NVV, n - v0);
+  const int tid = threadIdx.x;
+  const bool live = tid < nv;
+  const int4 q = c[v0 + (live ? tid : 0)];
   const int W4 = (W + 3) >> 2, H4 = (H + 3) >> 2, D4 = (D + 3) >> 2;
-  // the brick across a face in one axis: -1 / +1 when the coordinate is on the brick's low / high face, else none
-  auto side = [](int x) __attribute__((always_inline)) { return (x & 3) == 0 ? -1 : ((x & 3) == 3 ? 1 : 0); };
-  // candidate bricks: 8 tasks per voxel, 4 per thread, probed together (first probes issued at once; linear
-  // probing at load <= 0.5 resolves in ~1.5 rounds)
-  constexpr int NT = NV * 8 / 256;
-  uint64_t key[NT];
-  uint32_t slot[NT], ids[NT];
-  bool pend[NT];
+  const int ax = q.y & 3, ay = q.z & 3, az = q.w & 3;
+  // per axis: the face the voxel sits on (-1 low, +1 high, 0 none)
+  const int sx = ax == 0 ? -1 : (ax == 3 ? 1 : 0), sy = ay == 0 ? -1 : (ay == 3 ? 1 : 0),
+            sz = az == 0 ? -1 : (az == 3 ? 1 : 0);
+  uint64_t key[8];
+  uint32_t slot[8], ids[8];
+  bool pend[8];
 #pragma unroll
-  for (int u = 0; u < NT; u++) {
-    const int task = threadIdx.x + 256 * u, li = task >> 3, cb = task & 7;
-    const int4 q = cq[li < nv ? li : 0];
-    const int sx = (cb & 1) ? side(q.y) : 0, sy = (cb & 2) ? side(q.z) : 0, sz = (cb & 4) ? side(q.w) : 0;
-    const int bx = (q.y >> 2) + sx, by = (q.z >> 2) + sy, bz = (q.w >> 2) + sz;
-    const bool needed = ((cb & 1) == 0 || sx != 0) && ((cb & 2) == 0 || sy != 0) && ((cb & 4) == 0 || sz != 0);
-    pend[u] = li < nv && needed && bx >= 0 && bx < W4 && by >= 0 && by < H4 && bz >= 0 && bz < D4;
-    key[u] = (((uint64_t)(uint32_t)q.x * W4 + bx) * H4 + by) * D4 + bz;
-    slot[u] = pend[u] ? brick_home(key[u], mask) : 0u;
-    ids[u] = EMPTY;
+  for (int cb = 0; cb < 8; cb++) {
+    const int dx = (cb & 1) ? sx : 0, dy = (cb & 2) ? sy : 0, dz = (cb & 4) ? sz : 0;
+    const int bx = (q.y >> 2) + dx, by = (q.z >> 2) + dy, bz = (q.w >> 2) + dz;
+    const bool needed = ((cb & 1) == 0 || dx != 0) && ((cb & 2) == 0 || dy != 0) && ((cb & 4) == 0 || dz != 0);
+    pend[cb] = live && needed && bx >= 0 && bx < W4 && by >= 0 && by < H4 && bz >= 0 && bz < D4;
+    key[cb] = (((uint64_t)(uint32_t)q.x * W4 + bx) * H4 + by) * D4 + bz;
+    slot[cb] = pend[cb] ? brick_home(key[cb], mask) : 0u;
+    ids[cb] = EMPTY;
   }
   for (;;) {
     bool any = false;
 #pragma unroll
-    for (int u = 0; u < NT; u++) any |= pend[u];
+    for (int cb = 0; cb < 8; cb++) any |= pend[cb];
     if (!any) break;
-    ulonglong2 e[NT];
+    ulonglong2 e[8];
 #pragma unroll
-    for (int u = 0; u < NT; u++) e[u] = t[slot[u]];  // slot 0 (a valid entry) for finished tasks
+    for (int cb = 0; cb < 8; cb++) e[cb] = pend[cb] ? t[slot[cb]] : make_ulonglong2(0, 0);
 #pragma unroll
-    for (int u = 0; u < NT; u++) {
-      if (!pend[u]) continue;
-      if (e[u].x == key[u]) {
-        ids[u] = (uint32_t)e[u].y;
-        pend[u] = false;
-      } else if (e[u].x == HEMPTY) {
-        pend[u] = false;
+    for (int cb = 0; cb < 8; cb++) {
+      if (!pend[cb]) continue;
+      if (e[cb].x == key[cb]) {
+        ids[cb] = (uint32_t)e[cb].y;
+        pend[cb] = false;
+      } else if (e[cb].x == HEMPTY) {
+        pend[cb] = false;
       } else {
-        slot[u] = (slot[u] + 1) & mask;
+        slot[cb] = (slot[cb] + 1) & mask;
       }
     }
   }
+  // offset v = 9 (dx+1) + 3 (dy+1) + (dz+1): the brick bit of an axis is set when the step crosses the face the
+  // voxel sits on
+  uint32_t r[27];
 #pragma unroll
-  for (int u = 0; u < NT; u++) {
-    const int task = threadIdx.x + 256 * u;
-    (&bid[0][0])[task] = ids[u];
+  for (int v = 0; v < 27; v++) {
+    const int dx = v / 9 - 1, dy = v / 3 % 3 - 1, dz = v % 3 - 1;
+    const int x = q.y + dx, y = q.z + dy, z = q.w + dz;
+    const bool inb = live && x >= 0 && x < W && y >= 0 && y < H && z >= 0 && z < D;
+    // candidate brick by three selects with constant register indices (a runtime index would go to scratch)
+    const bool bx = dx != 0 && dx == sx, by = dy != 0 && dy == sy, bz = dz != 0 && dz == sz;
+    const uint32_t a0 = bx ? ids[1] : ids[0], a1 = bx ? ids[3] : ids[2], a2 = bx ? ids[5] : ids[4],
+                   a3 = bx ? ids[7] : ids[6];
+    const uint32_t b0 = by ? a1 : a0, b1 = by ? a3 : a2;
+    const uint32_t id = inb ? (bz ? b1 : b0) : EMPTY;
+    const uint32_t* p = bricks + (id != EMPTY ? (i64)id * 64 + brick_local(x, y, z) : 0);
+    r[v] = *p;  // entry 0 (a valid address) for misses
+    r[v] = id != EMPTY ? r[v] : EMPTY;
   }
-  __syncthreads();
-  // (voxel, offset) pairs p = threadIdx.x + 256 k: record addresses first, then every record load, then the
-  // stores and the mask bits. Offset v = 9 dx' + 3 dy' + dz' with v / 9 = (57 v) >> 9 and v / 3 = (11 v) >> 5
-  // for v < 27.
-  constexpr int NPR = (NV * 27 + 255) / 256;
-  i64 addr[NPR];
-  bool hit[NPR];
+  uint32_t g = 0;
 #pragma unroll
-  for (int k = 0; k < NPR; k++) {
-    const int p = threadIdx.x + 256 * k;
-    const int li = p / 27, v = p - li * 27;
-    const int4 q = cq[li < nv ? li : 0];
-    const int v9 = (v * 57) >> 9, v3 = (v * 11) >> 5;
-    const int x = q.y + v9 - 1, y = q.z + v3 - 3 * v9 - 1, z = q.w + v - 3 * v3 - 1;
-    const bool inb = p < nv * 27 && x >= 0 && x < W && y >= 0 && y < H && z >= 0 && z < D;
-    const int cb = ((x >> 2) != (q.y >> 2) ? 1 : 0) | ((y >> 2) != (q.z >> 2) ? 2 : 0) | ((z >> 2) != (q.w >> 2) ? 4 : 0);
-    const uint32_t id = inb ? bid[li][cb] : EMPTY;
-    hit[k] = id != EMPTY;
-    addr[k] = hit[k] ? (i64)id * 64 + brick_local(x, y, z) : 0;
+  for (int v = 0; v < 27; v++) {
+    g |= r[v] != EMPTY ? (1u << v) : 0u;
+    rows[tid * 27 + v] = r[v];
   }
-  uint32_t r[NPR];
-#pragma unroll
-  for (int k = 0; k < NPR; k++) r[k] = bricks[addr[k]];  // entry 0 (a valid address) for misses
-  // mask bits: a voxel's offsets are consecutive lanes, so the first lane of each voxel's run in a wavefront ORs
-  // the run's ballot bits (shifted to the run's first offset) into the voxel's mask: a few LDS atomics per
-  // wavefront instead of one per found neighbour (27 lanes on one address serialise)
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 0; k < NPR; k++) {
-    const int p = threadIdx.x + 256 * k;
-    const bool live = p < nv * 27;
-    const uint32_t rv = hit[k] ? r[k] : EMPTY;
-    if (live) nbr[v0 * 27 + p] = rv;
-    const uint64_t found = __ballot(live && rv != EMPTY);
-    const int li = p / 27, v = p - li * 27;
-    if (live && (v == 0 || lane == 0)) {
-      const int len = min(27 - v, 64 - lane);
-      const uint32_t bits = (uint32_t)((found >> lane) & ((1ull << len) - 1ull)) << v;
-      if (bits) atomicOr(&gm[li], bits);
-    }
-  }
-  __syncthreads();
-  if ((int)threadIdx.x < nv) {
-    uint32_t g = gm[threadIdx.x], b = g;
+  if (live) {
+    uint32_t b = g;
     b ^= b >> 1;
     b ^= b >> 2;
     b ^= b >> 4;
     b ^= b >> 8;
     b ^= b >> 16;
-    gray[v0 + threadIdx.x] = (int32_t)g;
-    bin[v0 + threadIdx.x] = b;
+    gray[v0 + tid] = (int32_t)g;
+    bin[v0 + tid] = b;
+  }
+  __syncthreads();
+  const int tot = nv * 27;
+  uint32_t* o = nbr + v0 * 27;
+#pragma unroll
+  for (int k = 0; k < 27; k++) {
+    const int i = k * NVV + tid;
+    if (i < tot) o[i] = rows[i];
   }
 }
 
@@ -366,9 +345,9 @@ SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep
                                               (uint4*)bricks.p);
   k_brick_fill<<<cdiv(n, 256), 256, 0, s>>>(coords.ptr<int4>(), n, W4, H4, D4, t, mask0, maskp,
                                             bricks.ptr<uint32_t>());
-  k_neighbors_brick<<<cdiv(n, NV), 256, 0, s>>>(coords.ptr<int4>(), n, W, H, D, t, mask0, maskp,
-                                                bricks.ptr<uint32_t>(), c.nbr.ptr<uint32_t>(),
-                                                c.gray.ptr<int32_t>(), bin.ptr<uint32_t>());
+  k_neighbors_vox<<<cdiv(n, NVV), NVV, 0, s>>>(coords.ptr<int4>(), n, W, H, D, t, mask0, maskp,
+                                               bricks.ptr<uint32_t>(), c.nbr.ptr<uint32_t>(),
+                                               c.gray.ptr<int32_t>(), bin.ptr<uint32_t>());
   CK(hipGetLastError());
   stable_argsort27(bin.ptr<uint32_t>(), n, c.sorted.ptr<int32_t>());
   c.W = W;
