@@ -50,6 +50,9 @@ def main():
                     help="skip the upsample-block and ConvNeXt-tail extras (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy (the counter calibration used by bench_profile.py)")
+    ap.add_argument("--kmap-only", action="store_true",
+                    help="only time the kernel-map build of the workload (--steps builds; the profiling command of the "
+                         "kernel-map summary)")
     args = ap.parse_args()
     if args.calibrate_copy:
         import torch
@@ -95,10 +98,10 @@ def main():
     act = sp.ACT_SILU if "silu" in cfg.epilogue else sp.ACT_NONE
     y = torch.empty((n, co), dtype=torch.bfloat16, device=dev)
 
-    # kernel-map build, timed separately (median of 5 after a warm-up)
+    # kernel-map build, timed separately (median after a warm-up)
     stream = torch.cuda.current_stream()
     map_ms = []
-    for i in range(6):
+    for i in range(1 + (args.steps if args.kmap_only else 5)):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         cache = sp.build_neighbors(tc)
@@ -106,6 +109,19 @@ def main():
         torch.cuda.synchronize()
         if i:
             map_ms.append(e0.elapsed_time(e1))
+    # algorithmic bytes of one build (once each): coords 16 B/voxel, table init + insert 12 B/slot at the reference's
+    # capacity (pow2 >= 2N), nbr 108 B/voxel, mask + decoded mask 8, sort in/out 8
+    cap = 1
+    while cap < 2 * n:
+        cap *= 2
+    map_bytes = n * (16 + 108 + 8 + 8) + cap * 12
+    map_med = float(np.median(map_ms))
+    kmap = {"ms": round(map_med, 4), "algorithmic_bytes": map_bytes,
+            "achieved_GBps": round(map_bytes / (map_med * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(map_bytes / (map_med * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    if args.kmap_only:
+        print(json.dumps({"workload": cfg.name, "N": n, "builds": len(map_ms), "kmap_build": kmap}), flush=True)
+        return
     nbr, gray, srt = cache.tensors()
     nbr_np = nbr.cpu().numpy()
     P = int((nbr_np != -1).sum())
@@ -308,7 +324,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "extras": {"mvox_per_s": round(mvox, 2), "compulsory_GBps": round(gbs, 1),
-                   "kmap_build_ms": round(float(np.median(map_ms)), 4), "first_call_ms": round(first_ms, 3),
+                   "kmap_build_ms": round(map_med, 4), "kmap_build": kmap, "first_call_ms": round(first_ms, 3),
                    "coord_gen_s": round(gen_s, 2),
                    "executed_over_active_pairs": round(executed_pairs / max(P, 1), 4), "skip_group_rows": gsz, "wall_s": round(wall, 3),
                    "upsample_block_e2e": e2e, "convnext_tail": tail, "measured_peaks": measured},
