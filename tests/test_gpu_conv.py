@@ -274,3 +274,51 @@ def test_halo_fallback_shuffled_rows(gpu):
     shuffled = c[rng.permutation(len(c))]
     for coords in (c, shuffled):
         run_case(gpu, coords, 64, 64, res_dt="bf16")
+
+
+@pytest.mark.parametrize("nrows", [25309, 22000, 23800])
+def test_wide_tail_split(gpu, nrows, monkeypatch):
+    """768 -> 768 (C2 coordinates, first nrows rows): 3 x ceil(nrows/128) tiles put 65-75 tiles on each XCD, more
+    than its 64 concurrent workgroups, so the wide kernel splits each XCD's last tiles over several workgroups along
+    K and reduces their fp32 partials. Split and unsplit schedules differ only in the fp32 summation order: fp32
+    outputs within rel-L2 1e-6, bf16 outputs within one bf16 ulp (+1e-5 absolute); the split result is checked against the oracle on
+    sampled rows (the rows of the split tiles included)."""
+    cfg = W.CONFIGS["c2"]
+    c = W.shell_coords(cfg)[:nrows]
+    n = len(c)
+    print(f"tail split case n={n}", flush=True)
+    w, b = W.conv_params(cfg)
+    tx, qx = quantize(W.features(n, cfg.ci, 11), "bf16")
+    tw, qw = quantize(w, "bf16")
+    tb, qb = quantize(b, "f32")
+    tr, qr = quantize(W.features(n, cfg.co, 12), "bf16")
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    args = (tx.to(gpu), tw.to(gpu), tb.to(gpu), cache)
+    rr = tr.to(gpu)
+    outs = {}
+    for split in (True, False):
+        if split:
+            monkeypatch.delenv("SPCONV_NO_SPLIT", raising=False)
+        else:
+            monkeypatch.setenv("SPCONV_NO_SPLIT", "1")
+        outs[split] = (sp.subm_conv_fused(*args, residual=rr, act=0, out_dtype=torch.float32),
+                       sp.subm_conv_fused(*args, residual=rr, act=0, out_dtype=torch.bfloat16))
+    monkeypatch.delenv("SPCONV_NO_SPLIT", raising=False)
+    (s32, s16), (u32, u16) = outs[True], outs[False]
+    rel = (torch.linalg.norm(s32 - u32) / torch.linalg.norm(u32)).item()
+    assert rel <= 1e-6, f"split vs unsplit fp32 rel-L2 {rel:.3g}"
+    assert torch.equal(s16, s32.to(torch.bfloat16)), "bf16 output is not round(fp32 output)"
+    d16 = (s16.float() - u16.float()).abs()
+    # one bf16 ulp of the value, plus 1e-5 absolute: near zero the fp32 reordering difference (~1e-6 of the partial
+    # sums' magnitude) exceeds the ulp of a tiny result
+    tol16 = torch.from_numpy(ulp(u16.float().cpu().numpy(), "bf16")).to(gpu) + 1e-5
+    assert torch.all(d16 <= tol16), f"split vs unsplit bf16: max diff {d16.max().item():.3g}"
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert not torch.equal(s32, u32), "expected the split schedule on a 256-CU part"
+    # oracle on sampled rows, including the last row tiles (the split ones sit at the end of each XCD's range)
+    rng = np.random.default_rng(5)
+    rows = np.unique(np.concatenate([rng.choice(n, size=800, replace=False), np.arange(n - 300, n)]))
+    nbr, _, _, _ = oracle.build_neighbors(c)
+    ref = oracle.conv(qx, qw, qb, nbr, res=qr, act=0, rows=rows)
+    sel = torch.from_numpy(rows).to(gpu)
+    compare(s32[sel], ref, "f32", f"split n={n}")

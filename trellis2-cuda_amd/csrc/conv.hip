@@ -119,6 +119,11 @@ struct ConvArgs {
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
   uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes, out_bytes, tbl_bytes;
+  // Tail split of the 256-channel wide kernel (part != nullptr): XCD x owns tiles [xt0[x], xt0[x+1]); the first
+  // xs of them run whole, each later one is split into xk[x] workgroups over its K stages, which write fp32
+  // partial tiles [BM][256] from slot xpart0[x] on; k_split_reduce sums them and applies the epilogue.
+  float* part;
+  int xt0[9], xk[8], xpart0[8], xs;
 };
 
 template <bool F16, int BM, int BN, int WGM, int WGN, int KC>
@@ -645,19 +650,14 @@ __device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
 // Weight repack for the narrow kernel: w [Co,27,Ci] -> per offset v, per 16-column tile t, per 32-channel step m,
 // one 1 KiB block of 64 lanes x 16 bytes in v_mfma_f32_16x16x32 operand order: lane l holds column t*16 + (l & 15),
 // input channels ((l >> 4)*S + m)*8 .. +8 (S = Ci/32 steps; lane quarter q owns channels q*8S .. q*8S + 8S).
-__global__ void k_pack_w_narrow(const u32x4* __restrict__ w, u32x4* __restrict__ wp, int Co, int Ci) {
-  const i64 q = (i64)blockIdx.x * blockDim.x + threadIdx.x;
-  const int S = Ci / 32, T = Co / 16;
-  const i64 total = (i64)Co * 27 * Ci / 8;
-  if (q >= total) return;
-  const int lane = (int)(q & 63);
-  i64 r = q >> 6;
-  const int m = (int)(r % S);
-  r /= S;
-  const int t = (int)(r % T);
-  const int v = (int)(r / T);
+// Grid (S, T, 27) of 64-thread blocks: block (m, t, v) writes destination block ((v*T + t)*S + m), so no thread
+// divides (the 64-bit division of a flat index cost more than the copy).
+__global__ void __launch_bounds__(64) k_pack_w_narrow(const u32x4* __restrict__ w, u32x4* __restrict__ wp, int Co,
+                                                      int Ci) {
+  const int S = Ci / 32, T = Co / 16, lane = threadIdx.x;
+  const int m = blockIdx.x, t = blockIdx.y, v = blockIdx.z;
   const int co = t * 16 + (lane & 15), ch = ((lane >> 4) * S + m) * 8;
-  wp[q] = w[((i64)co * 27 + v) * Ci / 8 + ch / 8];
+  wp[(((i64)v * T + t) * S + m) * 64 + lane] = w[((i64)co * 27 + v) * Ci / 8 + ch / 8];
 }
 
 // Narrow-channel kernel (Co = 16*T <= 64, Ci = 32*S <= 128): the layers that are bound by HBM traffic (gathers,
@@ -1153,7 +1153,23 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   __shared__ int vlist[32];
 
   const int g = blockIdx.x, per = a.grid / 8;
-  const int logical = (g % 8) * per + g / 8;
+  int logical, split = 0, nsplit = 1, pslot = -1;
+  if (a.part) {  // tail-split schedule: XCD x = g % 8 walks its own tiles, whole ones first, then the split pieces
+    const int x = g % 8, u = g / 8, c = a.xt0[x + 1] - a.xt0[x], kx = a.xk[x];
+    const int nfull = kx > 1 ? a.xs : c;
+    if (u < nfull) {
+      logical = a.xt0[x] + u;
+    } else {
+      const int q = u - nfull;
+      if (nfull + q / kx >= c) return;
+      logical = a.xt0[x] + nfull + q / kx;
+      split = q % kx;
+      nsplit = kx;
+      pslot = a.xpart0[x] + q;
+    }
+  } else {
+    logical = (g % 8) * per + g / 8;
+  }
   if (logical >= a.tiles_m * a.tiles_n) return;
   const int tm_ = logical / a.tiles_n, tn_ = logical % a.tiles_n;
   const int row0 = tm_ * BM, co0 = tn_ * (64 * NW);
@@ -1176,7 +1192,10 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   uint32_t mask = 0;
 #pragma unroll
   for (int i = 0; i < BM / 32; i++) mask |= gmask[i];
-  const int nvv = __popc(mask), total = nvv * nkc;
+  const int nvv = __popc(mask), all_stages = nvv * nkc;
+  // K stages [s0, s0 + total) of this workgroup: all of them, or its share of a split tile
+  const int s0 = (int)((long long)all_stages * split / nsplit);
+  const int total = (int)((long long)all_stages * (split + 1) / nsplit) - s0;
   if (tid < 27 && ((mask >> tid) & 1u)) vlist[__popc(mask & ((1u << tid) - 1u))] = tid;
   uint32_t gms[TM];
 #pragma unroll
@@ -1196,7 +1215,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   const uint32_t wslice = (uint32_t)((co0 >> 6) + wn) * 27u * (uint32_t)nkc;
   const uint32_t wlane = (uint32_t)lane * 16u;
 
-  int avi = 0, akc = 0, bvi = 0, bkc = 0, cvi = 0, ckc = 0;
+  int avi = s0 / nkc, akc = s0 % nkc, bvi = avi, bkc = akc, cvi = avi, ckc = akc;
   auto next = [&](int& vi, int& kc) __attribute__((always_inline)) {
     const bool wrap = kc + 1 == nkc;
     kc = wrap ? 0 : kc + 1;
@@ -1310,6 +1329,17 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
     }
   }
   wait_vmcnt<0>();
+  if (pslot >= 0) {  // a piece of a split tile: its fp32 partial sums go to the workspace, the reduction does the rest
+    float* pp = a.part + (size_t)pslot * (BM * 256);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int t = 0; t < TN; t++)
+#pragma unroll
+        for (int q = 0; q < 16; q++)
+          pp[(i * 32 + (q >> 2) * 8 + h * 4 + (q & 3)) * 256 + wn * 64 + t * 32 + l32] = acc[i][t][q];
+    return;
+  }
   __syncthreads();
 
   // epilogue through the (now idle) ring: one slot per wavefront
@@ -1327,6 +1357,64 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
 // 128-row tiles, two workgroups per CU. Measured on C3 (1526 tiles of 256 rows): 256-row tiles with one workgroup
 // per CU were 6% slower (prologue, barriers and epilogue exposed; 2x fewer weight loads per flop did not make up
 // for it), as were 8 wavefronts of 128 rows x 64 channels on a 256-row tile (3% slower: weights loaded twice).
+// Reduction of the split tiles: one thread per (row, 8 channels) of a split tile; sums its pieces' partials in
+// piece order, then the fused epilogue (bias, act, residual, one rounding) of the unsplit kernel.
+template <int BM>
+__global__ void __launch_bounds__(256) k_split_reduce(ConvArgs a) {
+  constexpr int UPT = BM * 256 / 8 / 256;  // workgroups per split tile
+  int st = blockIdx.x / UPT;                 // split tile, counted over the XCDs in order
+  const int e8 = (blockIdx.x % UPT) * 256 + threadIdx.x, r = e8 / 32, c8 = (e8 % 32) * 8;
+  int x = 0, ntail = 0;
+  for (; x < 8; x++) {
+    ntail = a.xk[x] > 1 ? (a.xt0[x + 1] - a.xt0[x]) - a.xs : 0;
+    if (st < ntail) break;
+    st -= ntail;
+  }
+  if (x == 8) return;
+  const int kx = a.xk[x], logical = a.xt0[x] + a.xs + st, pbase = a.xpart0[x] + st * kx;
+  const int tm_ = logical / a.tiles_n, tn_ = logical % a.tiles_n;
+  const int row = tm_ * BM + r, col = tn_ * 256 + c8;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < kx; j++) {
+    const float* pp = a.part + ((size_t)(pbase + j) * BM + r) * 256 + c8;
+    const f32x4 lo = *(const f32x4*)pp, hi = *(const f32x4*)(pp + 4);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      v[q] += lo[q];
+      v[q + 4] += hi[q];
+    }
+  }
+  const bool ok = row < a.N;
+  const Epi e = make_epi(a);
+  float bias8[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[col + q] : 0.f;
+  const uint32_t o = (uint32_t)(ok ? a.order[row] : 0) * (uint32_t)a.Co + (uint32_t)col;
+  u32x4 rv[2];
+  load_res8(e, o, ok, rv);
+  store_row8(e, o, ok, v, bias8, rv);
+}
+
+int device_cus() {
+  static int n[64] = {};
+  int dev = 0;
+  CK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) dev = 0;
+  if (!n[dev]) CK(hipDeviceGetAttribute(&n[dev], hipDeviceAttributeMultiprocessorCount, dev));
+  return n[dev];
+}
+
+// The tail split is off when SPCONV_NO_SPLIT is set (A/B runs and the tests that compare both schedules).
+bool split_enabled() {
+  const char* e = getenv("SPCONV_NO_SPLIT");
+  return !(e && e[0] && e[0] != '0');
+}
+
+// Wave-quantization tail: with two workgroups per CU, an XCD (32 CUs, its own L2; workgroup ids are dealt to the
+// 8 XCDs round-robin) runs 64 tiles at once. When an XCD's tiles number between 64 and 96 (C2: 594 tiles, 74-75
+// per XCD), the last ones would run as a thin second round; instead each of them is split over k = 64 / tail
+// (at most 8) workgroups along its K stages, so the second round is as wide as the first and k times shorter.
+// Measured on C2: 0.81 ms with 198 row tiles against 0.59 ms with 170 (510 workgroups, one round).
 template <bool F16>
 void launch_wide_dma(ConvArgs a) {
   constexpr int BM = 128;
@@ -1334,7 +1422,35 @@ void launch_wide_dma(ConvArgs a) {
   a.tiles_n = a.Co / 256;
   const int tiles = a.tiles_m * a.tiles_n;
   a.grid = (tiles + 7) / 8 * 8;
+  a.part = nullptr;
+  const int slots = 2 * (device_cus() / 8);  // concurrent workgroups per XCD
+  const int per = cdiv(tiles, 8);
+  Tensor ws;
+  if (split_enabled() && slots > 0 && per > slots && per - slots <= slots / 2) {
+    int units = 0, pslots = 0;
+    a.xs = slots;
+    for (int x = 0; x < 8; x++) {
+      a.xt0[x] = std::min(x * per, tiles);
+      const int c = std::min(per, tiles - a.xt0[x]), tail = c - slots;
+      a.xk[x] = tail > 0 ? std::min(8, slots / tail) : 1;
+      a.xpart0[x] = pslots;
+      if (a.xk[x] > 1) pslots += tail * a.xk[x];
+      units = std::max(units, a.xk[x] > 1 ? slots + tail * a.xk[x] : c);
+    }
+    a.xt0[8] = tiles;
+    if (pslots > 0) {
+      ws = empty({(i64)pslots * BM * 256}, F32);
+      a.part = ws.ptr<float>();
+      a.grid = 8 * units;
+    }
+  }
   k_conv_wide_dma<F16, BM><<<a.grid, 256, 0, stream()>>>(a);
+  if (a.part) {
+    int ntail = 0;
+    for (int x = 0; x < 8; x++)
+      if (a.xk[x] > 1) ntail += (a.xt0[x + 1] - a.xt0[x]) - a.xs;
+    k_split_reduce<BM><<<ntail * (BM * 256 / 8 / 256), 256, 0, stream()>>>(a);
+  }
 }
 
 template <bool F16, int NW, int BM>
@@ -1350,23 +1466,13 @@ void launch_wide(ConvArgs a) {
 // 64-channel input block kc, 32-column half t, step j), laid out as 64 lanes x 16 bytes in MFMA operand order:
 // lane l holds column c = slice*64 + t*32 + (l & 31), input channels kc*64 + (l >> 5)*32 + j*8 .. +8.
 // A wavefront then fetches a stage's weight fragment with fully coalesced 1 KiB loads.
-__global__ void k_pack_w(const u32x4* __restrict__ w, u32x4* __restrict__ wp, int Co, int Ci) {
-  const i64 q = (i64)blockIdx.x * blockDim.x + threadIdx.x;  // destination 16-byte chunk
-  const int nkc = Ci / 64;
-  const i64 total = (i64)Co * 27 * Ci / 8;
-  if (q >= total) return;
-  const int lane = (int)(q & 63);
-  i64 r = q >> 6;
-  const int j = (int)(r & 3);
-  r >>= 2;
-  const int t = (int)(r & 1);
-  r >>= 1;
-  const int kc = (int)(r % nkc);
-  r /= nkc;
-  const int v = (int)(r % 27);
-  const int slice = (int)(r / 27);
+// Grid (nkc*2, 27, Co/64) of 256-thread blocks: block (kc*2 + t, v, slice) writes the four 1 KiB blocks
+// j = 0..3 of that (slice, v, kc, t), thread = j*64 + lane; no thread divides.
+__global__ void __launch_bounds__(256) k_pack_w(const u32x4* __restrict__ w, u32x4* __restrict__ wp, int Co, int Ci) {
+  const int nkc = Ci / 64, kc = blockIdx.x >> 1, t = blockIdx.x & 1, v = blockIdx.y, slice = blockIdx.z;
+  const int j = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int co = slice * 64 + t * 32 + (lane & 31), ch = kc * 64 + (lane >> 5) * 32 + j * 8;
-  wp[q] = w[((i64)co * 27 + v) * Ci / 8 + ch / 8];
+  wp[((((i64)slice * 27 + v) * nkc + kc) * 2 + t) * 256 + threadIdx.x] = w[((i64)co * 27 + v) * Ci / 8 + ch / 8];
 }
 
 __global__ void k_to_f32(const void* p, int dt, int n, float* o) {
@@ -1514,7 +1620,6 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   Tensor wpack, mtbl;
   REQ(!row_map || reads_row_table(cfg, Ci, Co, act), "row map with a kernel that reads nbr directly");
   const bool compat = act & EPI_F16_COMPAT;
-  const i64 chunks = (i64)Co * 27 * Ci / 8;
   const SpConvCache::HaloTable* ht = nullptr;
   if (!compat && Co == 64 && Ci == 64 && halo_enabled()) {
     ht = &c.halo_table(HaloShape<2>::B, HaloShape<2>::UM);
@@ -1522,7 +1627,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   }
   if (ht) {  // halo kernel: narrow weight order, the tile's distinct neighbour rows copied to LDS once
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
-    k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
+    k_pack_w_narrow<<<dim3(Ci / 32, Co / 16, 27), 64, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
     a.hrows = ht->rows.ptr<int32_t>();
     a.hcount = ht->count.ptr<int32_t>();
@@ -1547,7 +1652,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     }
   } else if (!compat && Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, spatial row order
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
-    k_pack_w_narrow<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
+    k_pack_w_narrow<<<dim3(Ci / 32, Co / 16, 27), 64, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
     const SpConvCache::RowTable& rt = c.row_table(16);
     if (row_map) mtbl = c.mapped_table(16, *row_map, shift, M);
@@ -1557,7 +1662,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     a.tbl_bytes = (uint32_t)rt.tbl.bytes();
   } else if (!compat && cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
-    k_pack_w<<<cdiv(chunks, 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
+    k_pack_w<<<dim3(Ci / 64 * 2, 27, Co / 64), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
     if (Co % 256 == 0) {  // the 256 x 256 kernel reads its tiles' neighbour rows from the sorted-order table
       const SpConvCache::RowTable& rt = c.row_table(-1);
