@@ -3,8 +3,8 @@
 // so bits 27..31 are all zero and sorting 27 bits gives the same order).
 //
 // Three launches per pass over tiles of 256 x RCH keys (RCH = 4, 8 or 16, so there are at least ~512 tiles when
-// the input allows it) plus one zero fill for the whole sort:
-//   count      : per-tile digit counts, digit-major [512][ntiles]
+// the input allows it):
+//   count      : per-tile digit counts, digit-major [512][ntiles] (the first one also zeroes the digit-sum slots)
 //   digit scan : one workgroup per digit sums its row and publishes the sum; its start is the sum of the lower
 //                digits' published sums (read back all at once); the row is scanned in place to exclusive tile
 //                starts. One launch instead of a device-wide scan's three.
@@ -49,14 +49,15 @@ __device__ __forceinline__ void rank_chunks(const uint32_t* __restrict__ kin, co
   }
 }
 
-__global__ void k_rs_zero(uint32_t* __restrict__ p, i64 n) {
-  for (i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x) p[i] = 0;
-}
-
+// Per-tile digit counts. Workgroup 0 also zeroes `zero` (zn words: the digit-sum slots of every pass, before the
+// first digit scan reads them), which saves the sort a launch.
 template <int RCH>
 __global__ void __launch_bounds__(RT) k_rs_count(const uint32_t* __restrict__ keys, i64 n, int shift,
-                                                 uint32_t* __restrict__ hist, int ntiles) {
+                                                 uint32_t* __restrict__ hist, int ntiles, uint32_t* __restrict__ zero,
+                                                 int zn) {
   __shared__ uint32_t cnt[NBUK];
+  if (zero && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < zn; i += RT) zero[i] = 0;
   for (int d = threadIdx.x; d < NBUK; d += RT) cnt[d] = 0;
   __syncthreads();
   i64 base = (i64)blockIdx.x * (RT * RCH);
@@ -182,16 +183,17 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
   const i64 nh = (i64)NBUK * ntiles, swords = (i64)passes * NBUK * 2;
   Tensor hist = empty({nh + swords}, I32);  // nh is even: the 64-bit digit-sum slots stay 8-byte aligned
   uint64_t* dsum = (uint64_t*)(hist.ptr<uint32_t>() + nh);
-  k_rs_zero<<<1, 256, 0, s>>>((uint32_t*)dsum, swords);
   uint32_t* h = hist.ptr<uint32_t>();
   for (int p = 0; p < passes; p++) {
     uint32_t* kout;
     int32_t* vout;
     outs(p, kout, vout);
     const int shift = p * RBITS;
-    if (rch == 16) k_rs_count<16><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles);
-    else if (rch == 8) k_rs_count<8><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles);
-    else k_rs_count<4><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles);
+    uint32_t* z = p == 0 ? (uint32_t*)dsum : nullptr;  // the first count kernel zeroes every pass's digit sums
+    const int zn = (int)swords;
+    if (rch == 16) k_rs_count<16><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
+    else if (rch == 8) k_rs_count<8><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
+    else k_rs_count<4><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
     k_rs_digit_scan<<<NBUK, RT, 0, s>>>(h, dsum + p * NBUK, ntiles);
     if (rch == 16) k_rs_scatter<16><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, h, ntiles);
     else if (rch == 8) k_rs_scatter<8><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, h, ntiles);
