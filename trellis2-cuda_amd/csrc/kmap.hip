@@ -64,20 +64,17 @@ __device__ __forceinline__ uint32_t brick_find(const ulonglong2* __restrict__ t,
 __global__ void __launch_bounds__(256) k_brick_runs(const int4* __restrict__ c, i64 n, int W4, int H4, int D4,
                                                     uint32_t* __restrict__ part) {
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
-  const int lane = threadIdx.x & 63;
-  uint64_t k = HEMPTY;
+  int head = 0;
   if (i < n) {
     const int4 q = c[i];
-    k = brick_key(q.x, q.y, q.z, q.w, W4, H4, D4);
+    const uint64_t k = brick_key(q.x, q.y, q.z, q.w, W4, H4, D4);
+    if (i == 0) {
+      head = 1;
+    } else {
+      const int4 p = c[i - 1];
+      head = brick_key(p.x, p.y, p.z, p.w, W4, H4, D4) != k;
+    }
   }
-  // the previous row's key from the lane below; lane 0 reads its previous row itself
-  uint64_t kp = ((uint64_t)(uint32_t)__shfl_up((int)(uint32_t)(k >> 32), 1, 64) << 32) |
-                (uint32_t)__shfl_up((int)(uint32_t)k, 1, 64);
-  if (lane == 0 && i > 0 && i < n) {
-    const int4 p = c[i - 1];
-    kp = brick_key(p.x, p.y, p.z, p.w, W4, H4, D4);
-  }
-  const int head = i < n && (i == 0 || kp != k);
   const int cnt = __syncthreads_count(head);
   if (threadIdx.x == 0) part[blockIdx.x] = (uint32_t)cnt;
 }
