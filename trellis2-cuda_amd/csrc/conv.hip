@@ -1271,12 +1271,17 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
 #pragma unroll
       for (int k = (j * AL) / 4; k < ((j + 1) * AL) / 4; k++) dma(fill, k, off[k], ka);
       if (j + 1 < 4) read_j(fa[(j + 1) & 1], j + 1);
+      // raised wave priority over the MFMA burst: the sequencer keeps feeding this wave's matrix ops ahead of the
+      // other workgroup's memory instructions (C3 0.922 -> 0.915 ms, C2 0.755 -> 0.751, same box; priority 1 over
+      // the whole K loop instead was no better, C2 0.763; the halo kernel showed no change and does not do it)
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < TM; i++)
         if (gms[i] & vbit) {
 #pragma unroll
           for (int t = 0; t < TN; t++) acc[i][t] = mfma32<F16>(fa[j & 1][i], rb[t][j], acc[i][t]);
         }
+      __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int t = 0; t < TN; t++)
         rb[t][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, wlane + (t * 4 + j) * 1024, soff, 0);
