@@ -322,3 +322,33 @@ def test_wide_tail_split(gpu, nrows, monkeypatch):
     ref = oracle.conv(qx, qw, qb, nbr, res=qr, act=0, rows=rows)
     sel = torch.from_numpy(rows).to(gpu)
     compare(s32[sel], ref, "f32", f"split n={n}")
+
+
+def test_wide_tail_split_256_f16(gpu, monkeypatch):
+    """256 -> 256, fp16, bias + SiLU on the first 80000 rows of the C3 shell: 625 single-channel-tile row tiles,
+    79 per XCD (72 on the last), so the last 15 (8) tiles of each XCD are split along K over 4 (8) workgroups on a
+    256-CU part. Split vs unsplit fp32 outputs within
+    rel-L2 1e-6; the split result against the oracle on sampled rows and the last 500 rows."""
+    c = W.shell_coords(W.CONFIGS["c3"])[:80000]
+    n = len(c)
+    print(f"tail split case n={n} 256->256 f16", flush=True)
+    cfg = W.Config("t", 0, 0, (0, 0), False, 0, 256, 256, "f16", "", 31)
+    w, b = W.conv_params(cfg)
+    tx, qx = quantize(W.features(n, 256, 13), "f16")
+    tw, qw = quantize(w, "f16")
+    tb, qb = quantize(b, "f32")
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    args = (tx.to(gpu), tw.to(gpu), tb.to(gpu), cache)
+    monkeypatch.setenv("SPCONV_NO_SPLIT", "1")
+    u32 = sp.subm_conv_fused(*args, act=1, out_dtype=torch.float32)
+    monkeypatch.delenv("SPCONV_NO_SPLIT", raising=False)
+    s32 = sp.subm_conv_fused(*args, act=1, out_dtype=torch.float32)
+    s16 = sp.subm_conv_fused(*args, act=1, out_dtype=torch.float16)
+    rel = (torch.linalg.norm(s32 - u32) / torch.linalg.norm(u32)).item()
+    assert rel <= 1e-6, f"split vs unsplit fp32 rel-L2 {rel:.3g}"
+    assert torch.equal(s16, s32.to(torch.float16)), "fp16 output is not round(fp32 output)"
+    rng = np.random.default_rng(6)
+    rows = np.unique(np.concatenate([rng.choice(n, size=800, replace=False), np.arange(n - 500, n)]))
+    nbr, _, _, _ = oracle.build_neighbors(c)
+    ref = oracle.conv(qx, qw, qb, nbr, act=1, rows=rows)
+    compare(s32[torch.from_numpy(rows).to(gpu)], ref, "f32", f"split 256 n={n}")
