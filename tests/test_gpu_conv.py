@@ -10,6 +10,8 @@ Every case runs the kernel twice: with an fp32 output and with the case's output
     ~1.7e-3 relative L2 on N(0,1) data, and two fp32 sums that differ in the last bit can round to neighbouring
     bf16 values (1 ulp = 0.03125 on [4, 8)), so the dtype comparison cannot be tighter than that.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -149,25 +151,24 @@ def test_bad_arguments(gpu):
 
 
 @pytest.mark.parametrize("name", ["c2", "c3", "c4"])
-def test_configs_sampled_rows(gpu, name):
-    """Full-size workload on the GPU; 1500 seeded rows checked against the oracle."""
+def test_configs_all_rows(gpu, name):
+    """Full-size workload on the GPU, every output row checked against the (multithreaded) oracle."""
     cfg = W.CONFIGS[name]
     c = W.shell_coords(cfg)
-    rows = np.sort(np.random.default_rng(1).choice(len(c), size=min(1500, len(c)), replace=False))
     act = 1 if "silu" in cfg.epilogue else 0
     res = "bf16" if "res" in cfg.epilogue else None
-    run_case(gpu, c, cfg.ci, cfg.co, act=act, res_dt=res, rows=rows, seed=cfg.seed)
+    run_case(gpu, c, cfg.ci, cfg.co, act=act, res_dt=res, seed=cfg.seed)
 
 
 def test_c5_children(gpu):
+    """C5's children (the subdivided 1024^3 level, 128 -> 64, bias + SiLU), every output row checked."""
     cfg = W.CONFIGS["c5"]
     par = W.shell_coords(cfg)
     tc = torch.from_numpy(par).to(gpu)
     lg = W.keep_logits(len(par), cfg.keep_frac, cfg.seed)
     gc, _ = sp.subdivide(tc, torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16))
     c = gc.cpu().numpy()
-    rows = np.sort(np.random.default_rng(2).choice(len(c), size=1500, replace=False))
-    run_case(gpu, c, cfg.ci, cfg.co, act=1, rows=rows, seed=cfg.seed)
+    run_case(gpu, c, cfg.ci, cfg.co, act=1, seed=cfg.seed)
 
 
 def test_conv_golden_fixture(gpu):
@@ -281,9 +282,10 @@ def test_wide_tail_split(gpu, nrows, monkeypatch):
     """768 -> 768 (C2 coordinates, first nrows rows): 3 x ceil(nrows/128) tiles put 65-75 tiles on each XCD, more
     than its 64 concurrent workgroups, so the wide kernel splits each XCD's last tiles over several workgroups along
     K and reduces their fp32 partials. Split and unsplit schedules differ only in the fp32 summation order: fp32
-    outputs within rel-L2 1e-6, bf16 outputs within one bf16 ulp (+1e-5 absolute); the split result is checked against the oracle on
-    sampled rows (the rows of the split tiles included)."""
-    cfg = W.CONFIGS["c2"]
+    outputs within rel-L2 1e-6, bf16 outputs within one bf16 ulp (+1e-5 absolute); every row of the split result
+    is checked against the oracle. The coordinates are C2's spheres with a thicker shell (h = 2.35, 25 309 rows),
+    so that the row-tile counts reach the split range."""
+    cfg = dataclasses.replace(W.CONFIGS["c2"], half_thickness=2.35)
     c = W.shell_coords(cfg)[:nrows]
     n = len(c)
     print(f"tail split case n={n}", flush=True)
@@ -315,20 +317,16 @@ def test_wide_tail_split(gpu, nrows, monkeypatch):
     assert torch.all(d16 <= tol16), f"split vs unsplit bf16: max diff {d16.max().item():.3g}"
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
         assert not torch.equal(s32, u32), "expected the split schedule on a 256-CU part"
-    # oracle on sampled rows, including the last row tiles (the split ones sit at the end of each XCD's range)
-    rng = np.random.default_rng(5)
-    rows = np.unique(np.concatenate([rng.choice(n, size=800, replace=False), np.arange(n - 300, n)]))
     nbr, _, _, _ = oracle.build_neighbors(c)
-    ref = oracle.conv(qx, qw, qb, nbr, res=qr, act=0, rows=rows)
-    sel = torch.from_numpy(rows).to(gpu)
-    compare(s32[sel], ref, "f32", f"split n={n}")
+    ref = oracle.conv(qx, qw, qb, nbr, res=qr, act=0)
+    compare(s32, ref, "f32", f"split n={n}")
 
 
 def test_wide_tail_split_256_f16(gpu, monkeypatch):
     """256 -> 256, fp16, bias + SiLU on the first 80000 rows of the C3 shell: 625 single-channel-tile row tiles,
     79 per XCD (72 on the last), so the last 15 (8) tiles of each XCD are split along K over 4 (8) workgroups on a
     256-CU part. Split vs unsplit fp32 outputs within
-    rel-L2 1e-6; the split result against the oracle on sampled rows and the last 500 rows."""
+    rel-L2 1e-6; every row of the split result against the oracle."""
     c = W.shell_coords(W.CONFIGS["c3"])[:80000]
     n = len(c)
     print(f"tail split case n={n} 256->256 f16", flush=True)
@@ -347,8 +345,6 @@ def test_wide_tail_split_256_f16(gpu, monkeypatch):
     rel = (torch.linalg.norm(s32 - u32) / torch.linalg.norm(u32)).item()
     assert rel <= 1e-6, f"split vs unsplit fp32 rel-L2 {rel:.3g}"
     assert torch.equal(s16, s32.to(torch.float16)), "fp16 output is not round(fp32 output)"
-    rng = np.random.default_rng(6)
-    rows = np.unique(np.concatenate([rng.choice(n, size=800, replace=False), np.arange(n - 500, n)]))
     nbr, _, _, _ = oracle.build_neighbors(c)
-    ref = oracle.conv(qx, qw, qb, nbr, act=1, rows=rows)
-    compare(s32[torch.from_numpy(rows).to(gpu)], ref, "f32", f"split 256 n={n}")
+    ref = oracle.conv(qx, qw, qb, nbr, act=1)
+    compare(s32, ref, "f32", f"split 256 n={n}")

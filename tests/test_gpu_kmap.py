@@ -106,6 +106,18 @@ def test_kmap_sort_paths(gpu, n):
     check_map(c, gpu, B1s=(128,))
 
 
+@pytest.mark.parametrize("limit", ["0", "1"])
+def test_kmap_sort_unpublished_digit_sums(gpu, monkeypatch, limit):
+    """The sort's digit-scan workgroups wait a bounded number of polls for the lower digits' published sums and
+    then sum those digits' tile counts themselves. With the bound forced to 0 (every lower sum recomputed) or 1
+    (a mix of both paths) the order must stay bit-exact: the wait bound may never change the result."""
+    monkeypatch.setenv("SPCONV_SORT_SPIN_LIMIT", limit)
+    c = coords("c4")[:600000].copy()
+    c = c[np.random.default_rng(2).permutation(len(c))]
+    print(f"sort spin limit {limit} n={len(c)}", flush=True)
+    check_map(c, gpu, B1s=(128,))
+
+
 @pytest.mark.parametrize("name", ["c1", "c5"])
 def test_subdivide(gpu, name):
     par = coords(name)

@@ -6,8 +6,8 @@
 // the input allows it):
 //   count      : per-tile digit counts, digit-major [512][ntiles] (the first one also zeroes the digit-sum slots)
 //   digit scan : one workgroup per digit sums its row and publishes the sum; its start is the sum of the lower
-//                digits' published sums (read back all at once); the row is scanned in place to exclusive tile
-//                starts. One launch instead of a device-wide scan's three.
+//                digits' published sums (read back all at once); the row is scanned to exclusive tile starts.
+//                One launch instead of a device-wide scan's three.
 //   scatter    : each wavefront ranks its chunks of 64 keys in order; within a chunk, lanes holding the same digit
 //                find each other with 9 ballots (one per digit bit) and take rank = popcount(peers below me);
 //                wavefront counts are prefixed across the 4 wavefronts. Destination = tile start + wavefronts
@@ -19,7 +19,7 @@
 namespace {
 constexpr int RBITS = 9, NBUK = 1 << RBITS, RT = 256;
 constexpr uint64_t ST_SUM = 1ull << 32;  // published flag of a digit-sum slot
-constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kSpinLimit = 1u << 20;  // default bound of the digit-sum wait (SPCONV_SORT_SPIN_LIMIT)
 
 // Ranks a wavefront's RCH chunks of 64 keys (rows seg .. seg + RCH*64) by the digit at `shift`, in input order: lanes
 // holding the same digit find each other with RBITS ballots and take rank = popcount(peers below me) plus the
@@ -109,13 +109,17 @@ __global__ void __launch_bounds__(RT) k_rs_scatter(const uint32_t* __restrict__ 
 // Per-pass tile starts in one launch: workgroup d owns digit d. It sums its row of per-tile counts (digit-major,
 // [NBUK][ntiles]) and publishes the sum (flag in the high word of a zeroed 64-bit slot); the digit's start is the
 // sum of the lower digits' published sums, read back all at once (workgroups start in id order, so every lower
-// digit's workgroup is already running and publishes without waiting; the wait is bounded all the same). The row
-// is then scanned in place to exclusive tile starts.
-__global__ void __launch_bounds__(RT) k_rs_digit_scan(uint32_t* __restrict__ cnt, uint64_t* __restrict__ dsum,
-                                                      int ntiles) {
+// digit's workgroup is already running and publishes without waiting). The wait is bounded: a sum not published
+// within spin_limit polls is computed by the waiting workgroup from that digit's row of tile counts, so the
+// result never depends on the schedule (the limit only trades waiting against re-reading). The row is then
+// scanned to exclusive tile starts in `start` (not in place: the counts stay intact for such a fallback read).
+__global__ void __launch_bounds__(RT) k_rs_digit_scan(const uint32_t* __restrict__ cnt,
+                                                      uint32_t* __restrict__ start, uint64_t* __restrict__ dsum,
+                                                      int ntiles, uint32_t spin_limit) {
   __shared__ uint32_t red[RT / 64];
   const int d = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  uint32_t* row = cnt + (i64)d * ntiles;
+  const uint32_t* row = cnt + (i64)d * ntiles;
+  uint32_t* orow = start + (i64)d * ntiles;
   auto wg_sum = [&](uint32_t v) __attribute__((always_inline)) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
@@ -134,8 +138,15 @@ __global__ void __launch_bounds__(RT) k_rs_digit_scan(uint32_t* __restrict__ cnt
   uint32_t below = 0;
   for (int e = tid; e < d; e += RT) {
     uint64_t w = __hip_atomic_load(dsum + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (uint32_t spins = 0; (w >> 32) == 0 && spins < kSpinLimit; spins++)
+    for (uint32_t spins = 0; (w >> 32) == 0 && spins < spin_limit; spins++)
       w = __hip_atomic_load(dsum + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((w >> 32) == 0) {
+      // not published within the limit: sum digit e's row of tile counts here (they are complete: the count
+      // kernel ran before this launch), so the start is exact whatever the workgroup schedule
+      uint32_t s = 0;
+      for (int i = 0; i < ntiles; i++) s += cnt[(i64)e * ntiles + i];
+      w = s;
+    }
     below += (uint32_t)w;
   }
   uint32_t carry = wg_sum(below);
@@ -157,7 +168,7 @@ __global__ void __launch_bounds__(RT) k_rs_digit_scan(uint32_t* __restrict__ cnt
       if (w < wv) base += t;
       all += t;
     }
-    if (i < ntiles) row[i] = base + inc - v;
+    if (i < ntiles) orow[i] = base + inc - v;
     carry += all;
     __syncthreads();
   }
@@ -170,6 +181,10 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
   REQ(bits >= 1 && bits <= 32, "key bits %d", bits);
   const int passes = (bits + RBITS - 1) / RBITS;
   hipStream_t s = stream();
+  // SPCONV_SORT_SPIN_LIMIT overrides the digit-sum wait bound (0: every workgroup recomputes the lower digits' sums
+  // itself; the tests use it to check that path)
+  uint32_t spin_limit = kSpinLimit;
+  if (const char* e = getenv("SPCONV_SORT_SPIN_LIMIT")) spin_limit = (uint32_t)strtoul(e, nullptr, 10);
   Tensor kb0 = empty({n}, I32), kb1 = empty({n}, I32), vb0 = empty({n}, I32), vb1 = empty({n}, I32);
   // ping-pong buffers; the last pass writes its values straight into vals_out
   const uint32_t* kin = keys;
@@ -181,9 +196,11 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
   const int rch = n >= (i64)RT * 16 * 512 ? 16 : (n >= (i64)RT * 8 * 512 ? 8 : 4);
   const int ntiles = (int)cdiv(n, (i64)RT * rch);
   const i64 nh = (i64)NBUK * ntiles, swords = (i64)passes * NBUK * 2;
-  Tensor hist = empty({nh + swords}, I32);  // nh is even: the 64-bit digit-sum slots stay 8-byte aligned
-  uint64_t* dsum = (uint64_t*)(hist.ptr<uint32_t>() + nh);
+  // per-tile counts, tile starts, digit-sum slots (nh is even: the 64-bit slots stay 8-byte aligned)
+  Tensor hist = empty({2 * nh + swords}, I32);
+  uint64_t* dsum = (uint64_t*)(hist.ptr<uint32_t>() + 2 * nh);
   uint32_t* h = hist.ptr<uint32_t>();
+  uint32_t* st = h + nh;
   for (int p = 0; p < passes; p++) {
     uint32_t* kout;
     int32_t* vout;
@@ -194,10 +211,10 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
     if (rch == 16) k_rs_count<16><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
     else if (rch == 8) k_rs_count<8><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
     else k_rs_count<4><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
-    k_rs_digit_scan<<<NBUK, RT, 0, s>>>(h, dsum + p * NBUK, ntiles);
-    if (rch == 16) k_rs_scatter<16><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, h, ntiles);
-    else if (rch == 8) k_rs_scatter<8><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, h, ntiles);
-    else k_rs_scatter<4><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, h, ntiles);
+    k_rs_digit_scan<<<NBUK, RT, 0, s>>>(h, st, dsum + p * NBUK, ntiles, spin_limit);
+    if (rch == 16) k_rs_scatter<16><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles);
+    else if (rch == 8) k_rs_scatter<8><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles);
+    else k_rs_scatter<4><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles);
     kin = kout;
     vin = vout;
   }

@@ -36,13 +36,15 @@ class Config:
     keep_frac: float = 0.0
 
 
-# The five BASELINE configurations. Shape counts, radii and dtypes are the stated ones; the half-thickness h is
-# chosen per config so the voxel count lands near the stated size (counts are whatever the seed gives).
+# The five BASELINE configurations. Shape counts, radii and dtypes are the stated ones. Where a config states the
+# shell thickness it is used as stated: c2 |sdf| <= 1 (h = 1.0; 10 842 voxels with this seed, below the quoted
+# ~25k), c4 a 1-voxel shell (h = 0.5; 3.76 M voxels, P/N = 10.5). Where it does not (c1 ~5k, c3 ~400k, c5 ~800k
+# parents) h is chosen so the count lands near the stated size. Counts are whatever the seed gives.
 CONFIGS = {
     "c1": Config("c1", 32, 1, (12, 12), False, 1.5, 32, 32, "f32", "bias", 1001, centred=True),
-    "c2": Config("c2", 64, 6, (8, 20), False, 2.35, 768, 768, "bf16", "bias+res", 1002),
+    "c2": Config("c2", 64, 6, (8, 20), False, 1.0, 768, 768, "bf16", "bias+res", 1002),
     "c3": Config("c3", 256, 12, (20, 90), True, 0.8, 256, 256, "bf16", "bias+silu", 1003),
-    "c4": Config("c4", 1024, 16, (80, 350), False, 0.35, 64, 64, "bf16", "bias+res", 1004),
+    "c4": Config("c4", 1024, 16, (80, 350), False, 0.5, 64, 64, "bf16", "bias+res", 1004),
     "c5": Config("c5", 512, 12, (40, 170), False, 0.6, 128, 64, "bf16", "bias+silu", 1005,
                  subdivide=True, keep_frac=0.35),
 }
