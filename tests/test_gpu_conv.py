@@ -348,3 +348,71 @@ def test_wide_tail_split_256_f16(gpu, monkeypatch):
     nbr, _, _, _ = oracle.build_neighbors(c)
     ref = oracle.conv(qx, qw, qb, nbr, act=1)
     compare(s32, ref, "f32", f"split 256 n={n}")
+
+
+def split_vs_unsplit(gpu, monkeypatch, c, ci, co, dt, act, res_dt, seed, w256=True):
+    """Runs the conv with and without K splitting (SPCONV_NO_SPLIT), checks the two fp32 outputs agree to the fp32
+    summation order (rel-L2 1e-6), the 16-bit output is round(fp32), and every row of the split result against the
+    oracle. Returns whether the two schedules differed at all (they do when a split happened)."""
+    if w256:
+        monkeypatch.setenv("SPCONV_W256", "1")
+    n = len(c)
+    cfg = W.Config("t", 0, 0, (0, 0), False, 0, ci, co, dt, "", seed)
+    w, b = W.conv_params(cfg)
+    tx, qx = quantize(W.features(n, ci, seed + 1), dt)
+    tw, qw = quantize(w, dt)
+    tb, qb = quantize(b, "f32")
+    tr = qr = None
+    if res_dt:
+        tr, qr = quantize(W.features(n, co, seed + 2), res_dt)
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    args = (tx.to(gpu), tw.to(gpu), tb.to(gpu), cache)
+    rr = None if tr is None else tr.to(gpu)
+    monkeypatch.setenv("SPCONV_NO_SPLIT", "1")
+    u32 = sp.subm_conv_fused(*args, residual=rr, act=act, out_dtype=torch.float32)
+    monkeypatch.delenv("SPCONV_NO_SPLIT", raising=False)
+    s32 = sp.subm_conv_fused(*args, residual=rr, act=act, out_dtype=torch.float32)
+    s16 = sp.subm_conv_fused(*args, residual=rr, act=act, out_dtype=TDT[dt])
+    rel = (torch.linalg.norm(s32 - u32) / torch.linalg.norm(u32)).item()
+    assert rel <= 1e-6, f"split vs unsplit fp32 rel-L2 {rel:.3g}"
+    assert torch.equal(s16, s32.to(TDT[dt])), "16-bit output is not round(fp32 output)"
+    nbr, _, _, _ = oracle.build_neighbors(c)
+    ref = oracle.conv(qx, qw, qb, nbr, res=qr, act=act)
+    compare(s32, ref, "f32", f"split n={n} {ci}->{co}")
+    return not torch.equal(s32, u32)
+
+
+@pytest.mark.parametrize("nrows", [10842, 6000, 2000])
+def test_w256_k_split(gpu, monkeypatch, nrows):
+    """256 x 256 tile kernel (SPCONV_W256=1), 768 -> 768 bf16 with bias + residual on C2's shell (its first nrows
+    rows): 3 x ceil(nrows/256) tiles do not fill 256 CUs, so each tile's K stages are split over several workgroups and their fp32
+    partials summed by k_split_reduce256."""
+    c = W.shell_coords(W.CONFIGS["c2"])[:nrows]
+    print(f"w256 split case n={len(c)}", flush=True)
+    differed = split_vs_unsplit(gpu, monkeypatch, c, 768, 768, "bf16", 0, "bf16", 41)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert differed, "expected a K split on a 256-CU part"
+
+
+def test_w256_k_split_f16_silu(gpu, monkeypatch):
+    """256 x 256 tile kernel, 256 -> 512 fp16 with SiLU on the first 9000 rows of the C3 shell (36 x 2 tiles): K
+    split, two column tiles."""
+    c = W.shell_coords(W.CONFIGS["c3"])[:9000]
+    print(f"w256 split case n={len(c)} 256->512 f16", flush=True)
+    split_vs_unsplit(gpu, monkeypatch, c, 256, 512, "f16", 1, None, 43)
+
+
+def test_c3_w256_kernel(gpu, monkeypatch):
+    """The 256 x 256 tile kernel (SPCONV_W256=1) on the full C3 workload, every row against the oracle."""
+    monkeypatch.setenv("SPCONV_W256", "1")
+    cfg = W.CONFIGS["c3"]
+    run_case(gpu, W.shell_coords(cfg), cfg.ci, cfg.co, act=1, seed=cfg.seed)
+
+
+@pytest.mark.parametrize("ci,co", [(256, 256), (64, 256), (128, 768)])
+def test_w256_widths(gpu, monkeypatch, ci, co):
+    """256 x 256 tile kernel on a small shell (few tiles: K split) and every epilogue."""
+    monkeypatch.setenv("SPCONV_W256", "1")
+    c = shell(10.0)
+    run_case(gpu, c, ci, co, act=1, res_dt="bf16", seed=3)
+    run_case(gpu, c, ci, co, in_dt="f16", out_dt="f16", act=0, res_dt="f32", seed=4)

@@ -108,6 +108,7 @@ struct ConvArgs {
   const int32_t* hcount;
   const uint16_t* hidx;
   const uint32_t* hgm;
+  const int32_t* tsched;  // row tiles in dispatch order (SpConvCache::tile_schedule), for k_conv_w256
   const int32_t* rmap;  // gathered conv through the halo kernel: halo row h reads source row rmap[h] >> rshift
   int rshift, rmax;
   // skip residual (upsample block, halo kernel only): residual[i, c] = skip_x[src[i] >> 3, (src[i] & 7) * Cin/8 +
@@ -367,14 +368,14 @@ __device__ __forceinline__ void store_row8(const Epi& e, uint32_t o, bool ok, fl
 // Epilogue of one 32-row x 64-channel accumulator group, staged through LDS so every lane writes 16 contiguous
 // bytes: out[order[r], co] = act(acc + b) [+ residual]. `ew` is this wavefront's private [32][72] fp32 area.
 // Residual loads of one 32-row group (4 rows per lane slot p): RK 0 none, 1 fp32, 2 bf16/f16.
-template <int RK>
+template <int RK, bool NEG = false>
 __device__ __forceinline__ void load_group_res(const Epi& e, const int* tile_order, int rbase, int nrows, int Co,
                                                int col, int lane, u32x4 (&r)[4][2]) {
 #pragma unroll
   for (int p = 0; p < 4; p++) {
     const int rr = rbase + p * 8 + (lane >> 3);
     const uint32_t o = (uint32_t)tile_order[rr] * (uint32_t)Co + (uint32_t)col;
-    const bool ok = rr < nrows;
+    const bool ok = rr < nrows && (!NEG || tile_order[rr] >= 0);
     r[p][0] = r[p][1] = u32x4{0, 0, 0, 0};
     if constexpr (RK == 1) {
       r[p][0] = __builtin_amdgcn_raw_buffer_load_b128(e.res, ok ? o * 4u : kOutOfRange, 0, 0);
@@ -387,8 +388,8 @@ __device__ __forceinline__ void load_group_res(const Epi& e, const int* tile_ord
 
 // Epilogue of one 32-row x 64-channel accumulator group, staged through LDS so every lane writes 16 contiguous
 // bytes: out[order[r], co] = act(acc + b) [+ residual r]. `ew` is this wavefront's private [32][72] fp32 area.
-template <int TN>
-__device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TN], float* ew, const int* tile_order, int rbase,
+template <int TN, int TA = TN, int T0 = 0, bool NEG = false>
+__device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TA], float* ew, const int* tile_order, int rbase,
                                                int nrows, int col, const float (&bias8)[8], const Epi& e, int Co,
                                                int lane, const u32x4 (&r)[4][2]) {
   constexpr int ES = 72;  // row stride in floats: 4 rows apart differ by 32 banks, so the scatter is conflict-free
@@ -397,7 +398,7 @@ __device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TN], float* e
 #pragma unroll
   for (int t = 0; t < TN; t++)
 #pragma unroll
-    for (int i = 0; i < 16; i++) ew[((i >> 2) * 8 + h * 4 + (i & 3)) * ES + t * 32 + l32] = acc[t][i];
+    for (int i = 0; i < 16; i++) ew[((i >> 2) * 8 + h * 4 + (i & 3)) * ES + t * 32 + l32] = acc[T0 + t][i];
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
 #pragma unroll
@@ -406,7 +407,8 @@ __device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TN], float* e
     float v[8];
     *(f32x4*)&v[0] = *(const f32x4*)&ew[rr * ES + c8];
     *(f32x4*)&v[4] = *(const f32x4*)&ew[rr * ES + c8 + 4];
-    store_row8(e, (uint32_t)tile_order[rbase + rr] * (uint32_t)Co + (uint32_t)col, rbase + rr < nrows, v, bias8, r[p]);
+    const int orow = tile_order[rbase + rr];
+    store_row8(e, (uint32_t)orow * (uint32_t)Co + (uint32_t)col, rbase + rr < nrows && (!NEG || orow >= 0), v, bias8, r[p]);
   }
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
@@ -416,18 +418,21 @@ __device__ __forceinline__ void epilogue_group(const f32x16 (&acc)[TN], float* e
 // counter, so a residual load issued after a store cannot be waited for without also waiting for that store: the
 // residuals of group i+1 are therefore requested before the stores of group i, and a tile without a residual
 // issues no loads at all (its stores never hold the wavefront up).
-template <int TM, int TN>
-__device__ __forceinline__ void epilogue_tile(const f32x16 (&acc)[TM][TN], float* ew, const int* tile_order,
+// (TA: columns of the accumulator array; the tile's 64 channels are its columns T0 .. T0 + TN. NEG: rows whose
+// tile_order entry is negative are absent)
+template <int TM, int TN, int TA = TN, int T0 = 0, bool NEG = false>
+__device__ __forceinline__ void epilogue_tile(const f32x16 (&acc)[TM][TA], float* ew, const int* tile_order,
                                               int nrows, int co_w, const float (&bias8)[8], const Epi& e, int Co,
                                               int lane) {
   const int col = co_w + (lane & 7) * 8;
   auto run = [&](auto RKc) __attribute__((always_inline)) {
     constexpr int RK = decltype(RKc)::value;
     u32x4 r[2][4][2];
-    load_group_res<RK>(e, tile_order, 0, nrows, Co, col, lane, r[0]);
+    load_group_res<RK, NEG>(e, tile_order, 0, nrows, Co, col, lane, r[0]);
     static_for<TM>([&](auto I) __attribute__((always_inline)) {
-      if constexpr (I + 1 < TM) load_group_res<RK>(e, tile_order, (I + 1) * 32, nrows, Co, col, lane, r[(I + 1) & 1]);
-      epilogue_group<TN>(acc[I], ew, tile_order, I * 32, nrows, col, bias8, e, Co, lane, r[I & 1]);
+      if constexpr (I + 1 < TM)
+        load_group_res<RK, NEG>(e, tile_order, (I + 1) * 32, nrows, Co, col, lane, r[(I + 1) & 1]);
+      epilogue_group<TN, TA, T0, NEG>(acc[I], ew, tile_order, I * 32, nrows, col, bias8, e, Co, lane, r[I & 1]);
     });
   };
   if (e.res_dt < 0) run(std::integral_constant<int, 0>{});
@@ -1167,11 +1172,17 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
       nsplit = kx;
       pslot = a.xpart0[x] + q;
     }
+  } else if (a.tsched) {
+    // workgroups start in id order, dealt round-robin to the XCDs: row tiles longest first
+    // (SpConvCache::tile_schedule), so every XCD gets an even share of long and short tiles and the launch ends on
+    // short ones (the XCD-contiguous walk below leaves each XCD its densest tiles for last)
+    logical = g;
   } else {
     logical = (g % 8) * per + g / 8;
   }
   if (logical >= a.tiles_m * a.tiles_n) return;
-  const int tm_ = logical / a.tiles_n, tn_ = logical % a.tiles_n;
+  const int tm_ = a.tsched && !a.part ? a.tsched[logical / a.tiles_n] : logical / a.tiles_n;
+  const int tn_ = logical % a.tiles_n;
   const int row0 = tm_ * BM, co0 = tn_ * (64 * NW);
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), wn = wv;
@@ -1359,6 +1370,367 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   epilogue_tile<TM, TN>(acc, ew, ordT, nrows, co_w, bias8, e, a.Co, lane);
 }
 
+// 256 x 256 tile kernel (Co a multiple of 256, Ci a multiple of 64): one workgroup per CU, 4 wavefronts, each
+// owning all 256 rows x its own 64 output channels (8 x 2 tiles of v_mfma_f32_32x32x16, 256 accumulator registers).
+//  * Bytes per flop: a K stage (one offset x 64 input channels) reads 256 gathered rows and 256 weight columns of
+//    128 bytes for 2*256*256*64 flops -- half the weight bytes per flop of a 128-row tile.
+//  * Gathered rows go global -> LDS by DMA (buffer_load ... lds, 16 bytes per lane, 8 lanes per 128-byte row:
+//    whole cache lines; a 64-byte piece per row costs the address path as much as a whole line) into a 4-slot
+//    ring filled 3 stages ahead. Weights (distinct per wavefront) stream from L2 into operand registers one stage
+//    ahead, K-step-outer: step j's registers are refilled right after step j's MFMAs.
+//  * With one wavefront per SIMD every stall idles the matrix core, so the loop is software-pipelined across
+//    stage boundaries: the barrier that publishes stage s+1's slot sits before stage s's last K step, whose MFMAs
+//    then cover the latency of stage s+1's first fragment reads.
+//  * The loop's memory operations (fragment and index reads, DMAs, weight loads) are inline assembly with explicit
+//    counted waits: the compiler cannot tell the DMA into one ring slot from reads of another, and without that
+//    it waits for every DMA in flight before each read. Every load's output is early-clobber: a destination that
+//    shared a register with an address operand could be written by an earlier load's return before a later
+//    instruction of the same statement (stalled at issue) has read its address.
+//  * Slot layout: slot row q holds tile row q; its 16-byte piece p sits in unit p ^ ((q >> 1) & 7), so the fragment
+//    reads (32 rows, one piece) are conflict-free. A lane's 8 DMAs fill rows wv*64 + k*8 + (lane >> 3), k = 0..7;
+//    the offset-major index table stores row r at position pi(r) (pi transposes the 8 x 8 (k, m) blocks of each
+//    64-row block), so those 8 rows' neighbour indices are two 16-byte LDS reads.
+//  * No per-group MFMA skipping: the tile runs the union of its rows' offsets (EMPTY neighbours read past the
+//    buffer end and land as zeros); scalar branches between the MFMAs cost about what the skipped work saves.
+//  * Small row counts: a tile's K stages can be split over `ns` workgroups writing fp32 partial tiles, summed in
+//    piece order by k_split_reduce256 (which applies the epilogue), so a grid of few tiles still fills the CUs.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int w256_pi(int q) { return (q & ~63) | ((q & 7) << 3) | ((q >> 3) & 7); }
+template <int N>
+__device__ __forceinline__ void asm_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void asm_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+// Waits that also rewrite the registers the awaited loads fill ("+v"), in one volatile statement: the uses of those
+// registers cannot be scheduled above the wait.
+template <int N>
+__device__ __forceinline__ void lgkm_tie8(u32x4 (&A)[8]) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7])
+               : "n"(N) : "memory");
+}
+// (lgkmcnt counts at most 15 outstanding operations: the loop never has more than 10 in flight.)
+template <int N>
+__device__ __forceinline__ void lgkm_tie10(u32x4 (&A)[8], u32x4 (&B)[2]) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%10)"
+               : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]),
+                 "+v"(B[0]), "+v"(B[1])
+               : "n"(N) : "memory");
+}
+// MFMA as volatile inline assembly: keeps its place among the loop's other (inline-assembly) instructions, so the
+// fragment reads, DMAs and weight loads can be interleaved between the matrix instructions as written.
+template <bool F16>
+__device__ __forceinline__ void mfma_asm(f32x16& c, const u32x4& a, const u32x4& b) {
+  if constexpr (F16) asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+template <int N>
+__device__ __forceinline__ void vm_tie2(u32x4& a, u32x4& b) {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+
+template <bool F16>
+__global__ void __launch_bounds__(256, 1) k_conv_w256(ConvArgs a) {
+  constexpr int BM = 256, KC = 64, SU = BM * 8;  // rows per tile, channels per stage, 16-byte units per slot
+  __shared__ __attribute__((aligned(16))) u32x4 ring[4][SU];
+  __shared__ __attribute__((aligned(16))) uint32_t srcT[27 * BM];  // offset-major: srcT[v*256 + pi(tile row)]
+  __shared__ int ordP[BM];                                          // output row of tile row r (-1: none)
+  __shared__ uint32_t gmask[BM / 64];
+
+  // Workgroups start in id order, dealt round-robin to the XCDs; the row tiles are taken longest first
+  // (SpConvCache::tile_schedule), each row tile's column tiles and K pieces adjacent, so every XCD gets an even
+  // share of long and short tiles and the launch ends on short ones.
+  const int unit = blockIdx.x;
+  const int ns = a.xs > 0 ? a.xs : 1;  // K pieces per tile
+  const int tile = unit / ns, piece = unit % ns;
+  if (tile >= a.tiles_m * a.tiles_n) return;
+  const int tm_ = a.tsched[tile / a.tiles_n], tn_ = tile % a.tiles_n;
+  const int row0 = tm_ * BM;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = a.N, Ci = a.Ci, nkc = Ci / KC;
+
+  // prologue: this thread's tile row -> its 27 neighbour indices (offset-major), its output row at its slot row,
+  // and the tile's union mask
+  {
+    const __amdgpu_buffer_rsrc_t rt = make_rsrc(a.tbl, a.tbl_bytes);
+    const uint32_t base = (uint32_t)(row0 + tid) * 108u;  // the table is padded to a multiple of 256 rows
+    uint32_t nb[27];
+#pragma unroll
+    for (int v = 0; v < 27; v++) nb[v] = __builtin_amdgcn_raw_buffer_load_b32(rt, base + v * 4, 0, 0);
+    const int pr = w256_pi(tid);  // index-table position of tile row tid
+#pragma unroll
+    for (int v = 0; v < 27; v++) srcT[v * BM + pr] = nb[v];
+    ordP[tid] = row0 + tid < N ? a.order[row0 + tid] : -1;
+    uint32_t gm = a.gs[row0 + tid];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
+    if (lane == 0) gmask[wv] = gm;
+  }
+  __syncthreads();
+  const uint32_t mask = gmask[0] | gmask[1] | gmask[2] | gmask[3];
+  const int all_stages = __popc(mask) * nkc;
+  const int s0 = (int)((long long)all_stages * piece / ns);
+  const int total = (int)((long long)all_stages * (piece + 1) / ns) - s0;
+
+  f32x16 acc[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int t = 0; t < 2; t++) acc[i][t] = f32x16{};
+
+  if (total > 0) {
+    // buffer descriptors as plain SGPR quads for the inline assembly (same fields as make_rsrc)
+    auto rsrc4 = [](const void* p, uint32_t bytes) {
+      const uint64_t b = (uint64_t)(uintptr_t)p;
+      return i32x4{(int32_t)(uint32_t)b, (int32_t)(uint32_t)(b >> 32), (int32_t)bytes, 0x00020000};
+    };
+    const i32x4 rx = rsrc4(a.x, a.x_bytes), rw = rsrc4(a.w, a.w_bytes);
+    const uint32_t rowbytes = (uint32_t)Ci * 2u;
+    const uint32_t ring0 = (uint32_t)(size_t)(__attribute__((address_space(3))) u32x4*)&ring[0][0];
+    const uint32_t srct0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint32_t*)&srcT[0];
+    // DMA k of this lane: tile row wv*64 + (lane>>3)*8 + k into slot row q = (wv*8 + k)*8 + (lane>>3), piece
+    // (lane & 7) ^ ((q >> 1) & 7)
+    const uint32_t trow = (uint32_t)(wv * 64 + (lane >> 3) * 8);  // first of this lane's 8 tile rows
+    uint32_t apiece[2];                                            // piece byte offset for even / odd k
+#pragma unroll
+    for (int k = 0; k < 2; k++) apiece[k] = (uint32_t)(((lane & 7) ^ ((k * 4 + (lane >> 4)) & 7)) * 16);
+    const uint32_t dma_lds = ring0 + (uint32_t)(wv * 8 * 64) * 16u;  // + slot * 32 KB + k * 1 KB
+    // A fragment (group i, K step j): slot row i*32 + l32, piece j*2 + h
+    uint32_t alane[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) alane[j] = (uint32_t)(l32 * 128 + (((j * 2 + h) ^ ((l32 >> 1) & 7)) * 16));
+    // weights: 4 KB block per (32-column block, offset, 64-channel chunk); this wavefront's two blocks
+    const uint32_t wblk0 = (uint32_t)(tn_ * 8 + wv * 2) * 27u * (uint32_t)nkc;
+    const uint32_t wblk_t = 27u * (uint32_t)nkc * 4096u;
+    const uint32_t wlane = (uint32_t)lane * 16u;
+
+    uint32_t skip_m = mask;
+    for (int q = 0; q < s0 / nkc; q++) skip_m &= skip_m - 1u;
+    const int vlast = 31 - __builtin_clz(mask | 1u);
+    uint32_t dm = skip_m, bm = skip_m;  // offsets still to DMA (A) / to load (B)
+    int dkc = s0 % nkc, bkc = s0 % nkc;
+    auto advance = [&](uint32_t& m, int& kc, int& v, int& kcs) __attribute__((always_inline)) {
+      const bool live = m != 0;  // past the last stage: the last one again (harmless loads, exact wait counts)
+      v = __builtin_amdgcn_readfirstlane(live ? __builtin_ctz(m) : vlast);
+      kcs = live ? kc : nkc - 1;
+      const bool wrap = kc + 1 == nkc;
+      kc = wrap ? 0 : kc + 1;
+      if (wrap) m &= m - 1u;
+    };
+    // neighbour indices of this lane's 8 DMA rows for the next A stage, and that stage's channel-chunk offset
+    u32x4 idx[2];
+    int dka = 0;
+    auto read_idx = [&]() __attribute__((always_inline)) {
+      int v, kc;
+      advance(dm, dkc, v, kc);
+      dka = __builtin_amdgcn_readfirstlane(kc * KC * 2);
+      const uint32_t ad = srct0 + ((uint32_t)v * BM + trow) * 4u;
+      asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16" : "=&v"(idx[0]), "=&v"(idx[1]) : "v"(ad) : "memory");
+    };
+    uint32_t off[8];
+    int ka = 0;
+    auto make_off = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) off[k] = nbr_offset(idx[k >> 2][k & 3], rowbytes) + apiece[k & 1];
+      ka = dka;
+    };
+    auto dma = [&](int slot, int k) __attribute__((always_inline)) {
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(dma_lds + (uint32_t)slot * (SU * 16) + (uint32_t)k * 1024u);
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                   :: "s"(m0), "v"(off[k]), "s"(rx), "s"(ka) : "memory", "m0");
+    };
+    u32x4 rb[2][4];  // weights of the stage being computed: column block t, K step j
+    int bsoff = 0;
+    auto b_next = [&]() __attribute__((always_inline)) {
+      int v, kc;
+      advance(bm, bkc, v, kc);
+      bsoff = __builtin_amdgcn_readfirstlane((int)((wblk0 + (uint32_t)(v * nkc + kc)) * 4096u));
+    };
+    auto b_load = [&](int j) __attribute__((always_inline)) {
+      asm volatile("buffer_load_dwordx4 %0, %2, %3, %4 offen\n\tbuffer_load_dwordx4 %1, %2, %3, %5 offen"
+                   : "=&v"(rb[0][j]), "=&v"(rb[1][j])
+                   : "v"(wlane + j * 1024), "s"(rw), "s"(bsoff), "s"(bsoff + (int)wblk_t) : "memory");
+    };
+    u32x4 fa[2][8];  // A fragments of a K step (double-buffered)
+    auto read_a = [&](uint32_t slot_ad, int j, u32x4 (&A)[8]) __attribute__((always_inline)) {
+      const uint32_t ad = slot_ad + alane[j];
+#define SPC_READ_A(I) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(A[I]) : "v"(ad), "i"((I) * 4096) : "memory")
+      SPC_READ_A(0);
+      SPC_READ_A(1);
+      SPC_READ_A(2);
+      SPC_READ_A(3);
+      SPC_READ_A(4);
+      SPC_READ_A(5);
+      SPC_READ_A(6);
+      SPC_READ_A(7);
+#undef SPC_READ_A
+    };
+    // One K step: the 16 MFMAs of step j (fragments A, weights rb[.][j]), with the next step's 8 fragment reads
+    // (into An, from slot address nad, piece step jn) and the step's other memory work (work(p) after MFMA pair p)
+    // spread between them, so each is issued while a matrix instruction runs. A read names A[I] as an input and
+    // its output as early-clobber, so An[I] never shares registers with A[I]: an LDS return must not land in the
+    // operands of a matrix instruction that may still be reading them.
+    auto kstep = [&](const u32x4 (&A)[8], int j, u32x4 (&An)[8], uint32_t nad, int jn, auto&& work)
+                     __attribute__((always_inline)) {
+      const uint32_t ad = nad + alane[jn];
+#define SPC_KSTEP_PAIR(I)                                                                                 \
+      mfma_asm<F16>(acc[I][0], A[I], rb[0][j]);                                                          \
+      mfma_asm<F16>(acc[I][1], A[I], rb[1][j]);                                                          \
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(An[I]) : "v"(ad), "i"((I) * 4096), "v"(A[I]) : "memory"); \
+      work(I);
+      SPC_KSTEP_PAIR(0)
+      SPC_KSTEP_PAIR(1)
+      SPC_KSTEP_PAIR(2)
+      SPC_KSTEP_PAIR(3)
+      SPC_KSTEP_PAIR(4)
+      SPC_KSTEP_PAIR(5)
+      SPC_KSTEP_PAIR(6)
+      SPC_KSTEP_PAIR(7)
+#undef SPC_KSTEP_PAIR
+    };
+
+    // prologue: A(0..2) by DMA, B(0), indices for A(3); then publish slot 0 and read stage 0's first fragments
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+      read_idx();
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(idx[0]), "+v"(idx[1]) :: "memory");
+      make_off();
+#pragma unroll
+      for (int k = 0; k < 8; k++) dma(p, k);
+    }
+    b_next();
+#pragma unroll
+    for (int j = 0; j < 4; j++) b_load(j);
+    read_idx();
+    asm_vmcnt<24>();  // A0 landed (A1, A2, B0 may be in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(idx[0]), "+v"(idx[1]) :: "memory");
+    make_off();
+    wg_barrier();
+    read_a(ring0, 0, fa[0]);
+
+    // stage s (fragments of its K step 0 already requested): per K step j, wait for step j's fragments (requested a
+    // whole K step earlier), request step j+1's, MFMAs, two DMAs of A(s+3) into slot (s+3)%4, B(s+1) step j. Before
+    // the last step: wait for every read of slot s and the DMA of A(s+1), barrier, request stage s+1's step-0
+    // fragments.
+    // Stage 0 is peeled (FIRST): its weight waits count the prologue's loads, and a register-tied wait must not sit
+    // on a branch (the compiler would copy the awaited registers before it).
+    // Per stage s: K step j waits for its fragments (requested during step j-1) and weights, then runs kstep(), which
+    // requests step j+1's fragments (step 3: stage s+1's step 0, from the next slot, after the barrier); the DMAs of
+    // A(s+3) into slot (s+3)%4 go two per step, B(s+1) step j after step j's MFMAs.
+    auto stage = [&](int s, auto FIRSTc) __attribute__((always_inline)) {
+      constexpr bool FIRST = decltype(FIRSTc)::value;
+      const uint32_t cur = ring0 + (uint32_t)(s & 3) * (SU * 16), nxt = ring0 + (uint32_t)((s + 1) & 3) * (SU * 16);
+      const int fill = (s + 3) & 3;
+      b_next();
+      // B(s) step j was followed by 12 loads (stage 0: by 6 + 2j, the prologue's remaining B(0) loads and stage 0's)
+      lgkm_tie8<0>(fa[0]);
+      vm_tie2<FIRST ? 6 : 12>(rb[0][0], rb[1][0]);
+      kstep(fa[0], 0, fa[1], cur, 1, [&](int p) __attribute__((always_inline)) {
+        if (p == 3) dma(fill, 0);
+        if (p == 5) dma(fill, 1);
+        if (p == 7) b_load(0);
+      });
+
+      lgkm_tie8<0>(fa[1]);
+      vm_tie2<FIRST ? 8 : 12>(rb[0][1], rb[1][1]);
+      kstep(fa[1], 1, fa[0], cur, 2, [&](int p) __attribute__((always_inline)) {
+        if (p == 1) read_idx();  // indices of A(s+4)
+        if (p == 3) dma(fill, 2);
+        if (p == 5) dma(fill, 3);
+        if (p == 7) b_load(1);
+      });
+
+      lgkm_tie10<0>(fa[0], idx);  // step 2's fragments and the indices
+      vm_tie2<FIRST ? 10 : 12>(rb[0][2], rb[1][2]);
+      kstep(fa[0], 2, fa[1], cur, 3, [&](int p) __attribute__((always_inline)) {
+        if (p == 3) dma(fill, 4);
+        if (p == 5) dma(fill, 5);
+        if (p == 7) b_load(2);
+      });
+
+      lgkm_tie8<0>(fa[1]);  // step 3's fragments: every read of slot s is done
+      // A(s+1)'s last DMA was followed by 30 loads (stage 0: 28, stage 1: 36); no registers are tied here
+      if (FIRST) asm_vmcnt<28>(); else if (s == 1) asm_vmcnt<36>(); else asm_vmcnt<30>();
+      wg_barrier();
+      vm_tie2<12>(rb[0][3], rb[1][3]);
+      kstep(fa[1], 3, fa[0], nxt, 0, [&](int p) __attribute__((always_inline)) {
+        if (p == 3) dma(fill, 6);
+        if (p == 5) {
+          dma(fill, 7);
+          make_off();  // A(s+4)'s DMA offsets (after this stage's last DMAs read the previous ones)
+        }
+        if (p == 7) b_load(3);
+      });
+    };
+    stage(0, std::true_type{});
+#pragma nounroll
+    for (int s = 1; s < total; s++) stage(s, std::false_type{});
+    // The matrix instructions are inline assembly, so the compiler inserts no wait states between the last of them
+    // and the accumulator reads below: the results are written at the end of an MFMA's passes, so wait out the
+    // longest (a 32x32x16 MFMA is 8 passes of 4 cycles; 64 idle cycles cover it with margin).
+    asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+  }
+  asm_vmcnt<0>();
+  asm_lgkmcnt<0>();
+  __syncthreads();
+  if (a.part) {  // a K piece of a split tile: fp32 partial sums to the workspace, k_split_reduce256 does the rest
+    float* pp = a.part + (size_t)unit * (BM * 256);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int q = 0; q < 16; q++)
+          pp[(i * 32 + (q >> 2) * 8 + h * 4 + (q & 3)) * 256 + wv * 64 + t * 32 + l32] = acc[i][t][q];
+    return;
+  }
+  // epilogue through the idle ring: one slot per wavefront; slot rows map to output rows through ordP
+  float* ew = (float*)&ring[wv][0];
+  const int co_w = tn_ * 256 + wv * 64;
+  float bias8[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[co_w + (lane & 7) * 8 + q] : 0.f;
+  epilogue_tile<8, 2, 2, 0, true>(acc, ew, ordP, BM, co_w, bias8, make_epi(a), a.Co, lane);
+}
+
+// Sum of a split 256 x 256 tile's K pieces (in piece order), then the fused epilogue. One thread per (row, 8
+// channels); 32 workgroups per tile.
+__global__ void __launch_bounds__(256) k_split_reduce256(ConvArgs a) {
+  const int tile = blockIdx.x / 32, ns = a.xs;
+  const int e8 = (blockIdx.x % 32) * 256 + threadIdx.x, r = e8 / 32, c8 = (e8 % 32) * 8;
+  const int tm_ = a.tsched[tile / a.tiles_n], tn_ = tile % a.tiles_n;
+  const int row = tm_ * 256 + r, col = tn_ * 256 + c8;
+  // pieces of this tile: units tile*ns .. tile*ns + ns (the kernel's unit numbering)
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < ns; j++) {
+    const float* pp = a.part + ((size_t)(tile * ns + j) * 256 + r) * 256 + c8;
+    const f32x4 lo = *(const f32x4*)pp, hi = *(const f32x4*)(pp + 4);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      v[q] += lo[q];
+      v[q + 4] += hi[q];
+    }
+  }
+  const bool ok = row < a.N;
+  const Epi e = make_epi(a);
+  float bias8[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[col + q] : 0.f;
+  const uint32_t o = (uint32_t)(ok ? a.order[row] : 0) * (uint32_t)a.Co + (uint32_t)col;
+  u32x4 rv[2];
+  load_res8(e, o, ok, rv);
+  store_row8(e, o, ok, v, bias8, rv);
+}
+
 // 128-row tiles, two workgroups per CU. Measured on C3 (1526 tiles of 256 rows): 256-row tiles with one workgroup
 // per CU were 6% slower (prologue, barriers and epilogue exposed; 2x fewer weight loads per flop did not make up
 // for it), as were 8 wavefronts of 128 rows x 64 channels on a 256-row tile (3% slower: weights loaded twice).
@@ -1449,6 +1821,7 @@ void launch_wide_dma(ConvArgs a) {
       a.grid = 8 * units;
     }
   }
+  if (a.part) a.tsched = nullptr;  // the tail split keeps the XCD-contiguous walk
   k_conv_wide_dma<F16, BM><<<a.grid, 256, 0, stream()>>>(a);
   if (a.part) {
     int ntail = 0;
@@ -1456,6 +1829,61 @@ void launch_wide_dma(ConvArgs a) {
       if (a.xk[x] > 1) ntail += (a.xt0[x + 1] - a.xt0[x]) - a.xs;
     k_split_reduce<BM><<<ntail * (BM * 256 / 8 / 256), 256, 0, stream()>>>(a);
   }
+}
+
+// Weight repack for k_conv_w256: w [Co,27,Ci] -> one 4 KB block per (32-column block cb, offset v, 64-channel
+// chunk kc), inside it 4 K steps x 64 lanes x 16 bytes in v_mfma_f32_32x32x16 operand order: lane l of step j holds
+// column cb*32 + (l & 31), input channels kc*64 + j*16 + (l >> 5)*8 .. +8.
+// Grid (nkc, 27, Co/32) of 256-thread blocks: block (kc, v, cb), thread j*64 + lane.
+__global__ void __launch_bounds__(256) k_pack_w256(const u32x4* __restrict__ w, u32x4* __restrict__ wp, int Ci) {
+  const int nkc = Ci / 64, kc = blockIdx.x, v = blockIdx.y, cb = blockIdx.z;
+  const int j = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int co = cb * 32 + (lane & 31), ch = kc * 64 + j * 16 + (lane >> 5) * 8;
+  wp[(((i64)cb * 27 + v) * nkc + kc) * 256 + threadIdx.x] = w[((i64)co * 27 + v) * Ci / 8 + ch / 8];
+}
+
+// The 256 x 256 kernel (k_conv_w256) runs instead of the 128-row k_conv_wide_dma when SPCONV_W256 is set. Measured
+// on C3 (same box, both with longest-first tile order): 0.947 ms against 0.918 -- it halves the weight bytes per
+// flop, but one wavefront per SIMD exposes every per-stage wait, and without group skipping it runs the tile's
+// union of offsets (1.18x the active pairs against 1.05x).
+bool w256_enabled() {
+  const char* e = getenv("SPCONV_W256");
+  return e && e[0] && e[0] != '0';
+}
+
+// Tiles of 256 rows x 256 channels, one workgroup per CU. When the tiles fill the CUs poorly (small N, e.g. C2's
+// 43 x 3 tiles on 256 CUs), each tile's K stages are split over ns workgroups whose fp32 partials
+// k_split_reduce256 sums (ns from the cost model below).
+template <bool F16>
+void launch_w256(ConvArgs a) {
+  a.tiles_m = cdiv(a.N, 256);
+  a.tiles_n = a.Co / 256;
+  const int tiles = a.tiles_m * a.tiles_n, cus = device_cus();
+  // K pieces per tile: minimise rounds(ns) / ns x (a tile's time) + the partials' traffic (ns fp32 tiles written
+  // and read back), with a tile's time estimated from ~20 offsets x Ci/32 stages of ~0.53 us
+  int ns = 1;
+  if (split_enabled() && tiles < 2 * cus) {
+    const double t_tile = 20.0 * (a.Ci / 64) * 1.06e-6;
+    double best = 1e30;
+    for (int k = 1; k <= 8; k++) {
+      const double rounds = (double)cdiv(tiles * k, cus);
+      const double t = rounds / k * t_tile + (k > 1 ? 5e-6 + (double)k * tiles * 2 * 262144 / 4e12 : 0.0);
+      if (t < best * 0.97) {
+        best = t;
+        ns = k;
+      }
+    }
+  }
+  a.xs = ns;
+  Tensor ws;
+  a.part = nullptr;
+  if (ns > 1) {
+    ws = empty({(i64)tiles * ns * 256 * 256}, F32);
+    a.part = ws.ptr<float>();
+  }
+  a.grid = (tiles * ns + 7) / 8 * 8;
+  k_conv_w256<F16><<<a.grid, 256, 0, stream()>>>(a);
+  if (ns > 1) k_split_reduce256<<<tiles * 32, 256, 0, stream()>>>(a);
 }
 
 template <bool F16, int NW, int BM>
@@ -1509,6 +1937,7 @@ void dispatch(const SpConvCfg& cfg, ConvArgs a) {
     }
   }
   // Fixed tiles per channel width (no autotune): BM = 128 sorted rows per tile.
+  if (!compat && a.Co % 256 == 0 && a.Ci % 64 == 0 && w256_enabled()) return launch_w256<F16>(a);
   if (!compat && cfg.BK == 64 && a.Co % 256 == 0) return launch_wide_dma<F16>(a);
   if (!compat && cfg.BK == 64 && a.Co % 128 == 0) return launch_wide<F16, 2, 128>(a);
   if (a.Co % 128 == 0) {
@@ -1665,16 +2094,27 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
     a.gs = rt.gs.ptr<int32_t>();
     a.tbl_bytes = (uint32_t)rt.tbl.bytes();
+  } else if (!compat && Co % 256 == 0 && Ci % 64 == 0 && w256_enabled()) {  // 256 x 256 tiles: 4 KB weight blocks
+    wpack = empty({(i64)Co * 27 * Ci}, x.dt);
+    k_pack_w256<<<dim3(Ci / 64, 27, Co / 32), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Ci);
+    a.w = wpack.ptr<uint16_t>();
+    const SpConvCache::RowTable& rt = c.row_table(-1);
+    if (row_map) mtbl = c.mapped_table(-1, *row_map, shift, M);
+    a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
+    a.gs = rt.gs.ptr<int32_t>();
+    a.tbl_bytes = (uint32_t)rt.tbl.bytes();
+    a.tsched = c.tile_schedule(-1, 256).ptr<int32_t>();
   } else if (!compat && cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w<<<dim3(Ci / 64 * 2, 27, Co / 64), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
-    if (Co % 256 == 0) {  // the 256 x 256 kernel reads its tiles' neighbour rows from the sorted-order table
+    if (Co % 256 == 0) {  // the 128 x 256 kernel reads its tiles' neighbour rows from the sorted-order table
       const SpConvCache::RowTable& rt = c.row_table(-1);
       if (row_map) mtbl = c.mapped_table(-1, *row_map, shift, M);
       a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
       a.gs = rt.gs.ptr<int32_t>();
       a.tbl_bytes = (uint32_t)rt.tbl.bytes();
+      a.tsched = c.tile_schedule(-1, 128).ptr<int32_t>();
     }
   }
   REQ(!skip || ht, "the fused skip residual needs the halo kernel");

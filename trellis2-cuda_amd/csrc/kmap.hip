@@ -527,6 +527,74 @@ const SpConvCache::RowTable& SpConvCache::row_table(int log2w) {
   return rtab.emplace(key, r).first->second;
 }
 
+// Per tile of B rows of a tile-order mask array (padded to a multiple of B): the number of offsets in the OR of
+// its rows' masks. One workgroup of B threads per tile.
+__global__ void __launch_bounds__(256) k_tile_cost(const int32_t* __restrict__ gs, int B, uint32_t* __restrict__ cost) {
+  __shared__ uint32_t part[4];
+  uint32_t m = (uint32_t)gs[(i64)blockIdx.x * B + threadIdx.x];
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) m |= (uint32_t)__shfl_xor((int)m, d, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t u = 0;
+    for (int w = 0; w < (int)(blockDim.x + 63) / 64; w++) u |= part[w];
+    cost[blockIdx.x] = (uint32_t)__popc(u);
+  }
+}
+
+// Tile ids ordered by cost, largest first (counting sort over the 28 possible costs; ties keep tile order). One
+// workgroup.
+__global__ void __launch_bounds__(1024) k_tile_lpt(const uint32_t* __restrict__ cost, int nt, int32_t* __restrict__ order) {
+  __shared__ uint32_t cnt[32], start[32];
+  if (threadIdx.x < 32) cnt[threadIdx.x] = 0;
+  __syncthreads();
+  for (int t = threadIdx.x; t < nt; t += blockDim.x) atomicAdd(&cnt[27 - min(cost[t], 27u)], 1u);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t run = 0;
+    for (int c = 0; c < 32; c++) {
+      start[c] = run;
+      run += cnt[c];
+    }
+  }
+  __syncthreads();
+  // stable placement: each bucket is filled in tile order by one pass per chunk of 1024 tiles, ranking a tile
+  // among the chunk's tiles of its bucket with a block-wide count of the lower-numbered ones
+  __shared__ uint32_t key[1024];
+  for (int base = 0; base < nt; base += 1024) {
+    const int t = base + (int)threadIdx.x;
+    const uint32_t k = t < nt ? 27 - min(cost[t], 27u) : 31u;
+    key[threadIdx.x] = k;
+    __syncthreads();
+    uint32_t rank = 0;
+    for (int u = 0; u < (int)threadIdx.x; u++) rank += key[u] == k;
+    if (t < nt) order[start[k] + rank] = t;
+    __syncthreads();
+    // advance the bucket starts by this chunk's counts
+    if (threadIdx.x < 32) {
+      uint32_t c = 0;
+      for (int u = 0; u < 1024; u++) c += key[u] == threadIdx.x;
+      start[threadIdx.x] += c;
+    }
+    __syncthreads();
+  }
+}
+
+const Tensor& SpConvCache::tile_schedule(int log2w, int B) {
+  const auto key = std::make_pair(log2w < 0 ? -1 : log2w, B);
+  auto it = tsched.find(key);
+  if (it != tsched.end()) return it->second;
+  REQ(B > 0 && B <= 256 && B % 64 == 0 && kRowTablePad % B == 0, "tile rows %d", B);
+  const RowTable& rt = row_table(log2w);
+  const i64 nt = std::max<i64>(cdiv(N, B), 1);
+  Tensor cost = empty({nt}, I32), order = empty({nt}, I32);
+  k_tile_cost<<<(unsigned)nt, B, 0, stream()>>>(rt.gs.ptr<int32_t>(), B, cost.ptr<uint32_t>());
+  k_tile_lpt<<<1, 1024, 0, stream()>>>(cost.ptr<uint32_t>(), (int)nt, order.ptr<int32_t>());
+  CK(hipGetLastError());
+  return tsched.emplace(key, order).first->second;
+}
+
 // mapped rows outside [0, m) become EMPTY, so the conv reads zeros for them
 __global__ void k_map_table(const uint32_t* __restrict__ tbl, i64 entries, const int32_t* __restrict__ row_map,
                             int shift, uint32_t m, uint32_t* __restrict__ out) {

@@ -36,6 +36,11 @@ struct SpConvCache {
   };
   std::map<int, RowTable> rtab;
   const RowTable& row_table(int log2w);
+  // Tiles of B consecutive entries of row_table(log2w) in dispatch order: longest first (by the number of offsets
+  // in the tile's union mask, the tile's K stages), so the last workgroups of a launch are the short ones.
+  // Memoized per (log2w, B).
+  std::map<std::pair<int, int>, Tensor> tsched;
+  const Tensor& tile_schedule(int log2w, int B);
   // row_table(log2w).tbl with every non-EMPTY entry r replaced by row_map[r] >> shift, or EMPTY when that is not
   // below m (not memoized: row_map is the caller's). Used by the gathered conv.
   Tensor mapped_table(int log2w, const Tensor& row_map, int shift, i64 m);

@@ -346,3 +346,17 @@ def subdivide(coords, logits_f16):
     m = ctypes.c_int64()
     _check(load_library().spc_subdivide(_ptr(coords), _ptr(logits_f16), n, _ptr(cc), _ptr(src), ctypes.byref(m)))
     return cc[:m.value], src[:m.value]
+
+
+def source_digest() -> str:
+    """sha256 over the HIP/C++ sources of the library (file names and contents, sorted): stamps measured profile
+    figures with the code they were measured on, so a stale figure can be recognised."""
+    import hashlib
+    d = os.path.join(_PKG, "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(d)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(d, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
