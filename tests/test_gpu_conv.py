@@ -268,13 +268,63 @@ def test_f16_compat_epilogue(gpu, ci, co):
 
 def test_halo_fallback_shuffled_rows(gpu):
     """64 -> 64 on a shell whose rows are shuffled: every 256-row window then reads far more than 512 distinct
-    neighbour rows, so the halo schedule reports overflow and the conv runs on the gathering kernel -- same
-    results either way (checked against the oracle); the unshuffled shell takes the halo kernel."""
+    neighbour rows, so every tile is a spill tile and the gathering kernel computes all rows -- same results
+    either way (checked against the oracle); the unshuffled shell takes the halo kernel."""
     c = shell(12.0)
     rng = np.random.default_rng(4)
     shuffled = c[rng.permutation(len(c))]
     for coords in (c, shuffled):
         run_case(gpu, coords, 64, 64, res_dt="bf16")
+
+
+def mixed_spill_coords():
+    """A sparse sphere shell plus a dense 12^3 block, Morton-sorted: the block's 256-row windows are 8x8x4 bricks
+    whose 10x10x6 halos (600 rows) exceed the 512-row LDS halo, so those tiles spill to the gathering kernel while
+    the shell's tiles stay on the halo kernel."""
+    s = shell(10.0, grid=26)
+    g = np.stack(np.meshgrid(*(np.arange(30, 42),) * 3, indexing="ij"), -1).reshape(-1, 3)
+    p = np.concatenate([s[:, 1:], g]).astype(np.int64)
+    p = p[np.argsort(W.morton3(p[:, 0], p[:, 1], p[:, 2]), kind="stable")]
+    return np.concatenate([np.zeros((len(p), 1), np.int64), p], 1).astype(np.int32)
+
+
+def test_halo_spill_tiles(gpu):
+    """Spill tiles of the halo schedule run on the gathering kernel, the rest on the halo kernel: every row checked
+    against the oracle, with and without SiLU / residual, and the tail tile partial."""
+    c = mixed_spill_coords()
+    run_case(gpu, c, 64, 64, res_dt="bf16")
+    run_case(gpu, c, 64, 64, act=1, out_dt="f32")
+    run_case(gpu, c[:4092], 64, 64, res_dt="bf16", seed=3)  # the last tile partial (252 rows) and a spill tile
+
+
+def test_halo_spill_gathered_and_skip(gpu):
+    """Gathered conv (row map) and the upsample skip on a cache with spill tiles: the gathered conv equals the conv
+    of the materialized rows bit for bit (the spill tiles read their rows through the map too), and the skip
+    variant equals conv + add_skip bit for bit (it takes the unfused path when tiles spill)."""
+    c = mixed_spill_coords()
+    n = len(c)
+    m = n // 2 + 5
+    g = torch.Generator().manual_seed(5)
+    xs = torch.randn((m, 64), generator=g).to(torch.bfloat16).to(gpu)
+    rmap = torch.randint(-8, 8 * m + 40, (n,), generator=g, dtype=torch.int32).to(gpu)
+    w, b = W.conv_params(W.Config("t", 0, 0, (0, 0), False, 0, 64, 64, "bf16", "", 51))
+    ws, bs = torch.from_numpy(w).to(torch.bfloat16).to(gpu), torch.from_numpy(b).to(gpu)
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    y1 = sp.subm_conv_gathered(xs, rmap, 3, ws, bs, cache, act=1, out_dtype=torch.float32)
+    idx = rmap.long() >> 3
+    ok = (idx >= 0) & (idx < m)
+    xg = torch.zeros((n, 64), dtype=torch.bfloat16, device=gpu)
+    xg[ok] = xs[idx[ok]]
+    y2 = sp.subm_conv_fused(xg, ws, bs, cache, act=1, out_dtype=torch.float32)
+    assert torch.equal(y1, y2), "gathered != materialized on a cache with spill tiles"
+    nbr, _, _, _ = oracle.build_neighbors(c)
+    wq = torch.from_numpy(w).to(torch.bfloat16).float().numpy()
+    compare(y1, oracle.conv(xg.float().cpu().numpy(), wq, b, nbr, act=1), "f32", "spill gathered")
+    src = torch.randint(0, 8 * m, (n,), generator=g, dtype=torch.int32).to(gpu)
+    y3 = sp.subm_conv_skip(xg, ws, bs, cache, xs, src, act=1)
+    y4 = sp.subm_conv_fused(xg, ws, bs, cache, act=1)
+    sp.add_skip(y4, xs, src)
+    assert torch.equal(y3, y4), "skip variant != conv + add_skip on a cache with spill tiles"
 
 
 @pytest.mark.parametrize("nrows", [25309, 22000, 23800])

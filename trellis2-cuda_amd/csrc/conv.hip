@@ -938,6 +938,7 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
   const int wr = wv / WC, wc = wv % WC;
   const int N = a.N;
   const int U = __builtin_amdgcn_readfirstlane(a.hcount[tile]);
+  if (U < 0) return;  // a spill tile (more distinct rows than UM): the gathering kernel computes its rows
 
   // prologue: index table and halo rows by DMA, the zero row and the group masks by plain stores
   {
@@ -2117,10 +2118,31 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       a.tsched = c.tile_schedule(-1, 128).ptr<int32_t>();
     }
   }
-  REQ(!skip || ht, "the fused skip residual needs the halo kernel");
+  REQ(!skip || (ht && ht->spill_n == 0), "the fused skip residual needs the halo kernel with no spill tiles");
   if (x.dt == F16) dispatch<true>(cfg, a);
   else dispatch<false>(cfg, a);
   CK(hipGetLastError());
+  if (ht && ht->spill_n > 0) {  // the halo kernel skipped the spill tiles: their positions go to the gathering kernel
+    ConvArgs sa = a;
+    sa.hrows = nullptr;
+    sa.hcount = nullptr;
+    sa.hidx = nullptr;
+    sa.hgm = nullptr;
+    sa.rmap = nullptr;
+    sa.N = (int)ht->spill_n;
+    sa.order = ht->spill.order.ptr<int32_t>();
+    sa.gs = ht->spill.gs.ptr<int32_t>();
+    sa.tbl = ht->spill.tbl.ptr<uint32_t>();
+    sa.tbl_bytes = (uint32_t)ht->spill.tbl.bytes();
+    if (row_map) {
+      mtbl = empty(ht->spill.tbl.sh, I32);
+      map_table_rows(ht->spill.tbl, *row_map, shift, M, mtbl);
+      sa.tbl = mtbl.ptr<uint32_t>();
+    }
+    if (x.dt == F16) launch_narrow<true, 2, 4>(sa);
+    else launch_narrow<false, 2, 4>(sa);
+    CK(hipGetLastError());
+  }
 }
 
 void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, const Tensor& x_skip,
@@ -2135,7 +2157,10 @@ void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, 
   REQ((uint64_t)x_skip.bytes() <= kMaxBufferBytes && ((uintptr_t)x_skip.p % 16) == 0, "x_skip too large / unaligned");
   REQ(!(act & EPI_F16_COMPAT), "no fp16-compatible epilogue with the fused skip");
   bool fused = c.N > 0 && Ci == 64 && Co == 64 && halo_enabled();
-  if (fused) fused = c.halo_table(HaloShape<2>::B, HaloShape<2>::UM).ok;
+  if (fused) {
+    const SpConvCache::HaloTable& ht = c.halo_table(HaloShape<2>::B, HaloShape<2>::UM);
+    fused = ht.ok && ht.spill_n == 0;
+  }
   if (fused) {
     const SkipRes sk{&x_skip, &src};
     conv_impl(x, nullptr, 0, w, b, nullptr, act, c, out, &sk);

@@ -487,12 +487,13 @@ const Tensor& SpConvCache::window_order(int log2w) {
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 __global__ void __launch_bounds__(256) k_row_table(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ gray,
-                                                   const int32_t* __restrict__ order, i64 n, i64 npad,
+                                                   const int32_t* __restrict__ order, i64 nsrc, i64 n, i64 npad,
                                                    uint32_t* __restrict__ tbl, int32_t* __restrict__ gs) {
+  // nsrc: rows of nbr; n: live positions of order (the rest of the npad positions are padding)
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= npad) return;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(nbr), 0,
-                                                                      (int)(n * 108), 0x00020000);
+                                                                      (int)(nsrc * 108), 0x00020000);
   const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(tbl, 0, (int)(npad * 108), 0x00020000);
   const bool live = i < n;
   const int o = live ? order[i] : 0;
@@ -521,7 +522,7 @@ const SpConvCache::RowTable& SpConvCache::row_table(int log2w) {
   r.gs = empty({npad}, I32);
   REQ(npad * 108 <= 0xfffe0000ll, "neighbour table of %lld rows too large", (long long)npad);
   k_row_table<<<cdiv(npad, 256), 256, 0, stream()>>>(nbr.ptr<uint32_t>(), gray.ptr<int32_t>(),
-                                                          r.order.ptr<int32_t>(), N, npad, r.tbl.ptr<uint32_t>(),
+                                                          r.order.ptr<int32_t>(), N, N, npad, r.tbl.ptr<uint32_t>(),
                                                           r.gs.ptr<int32_t>());
   CK(hipGetLastError());
   return rtab.emplace(key, r).first->second;
@@ -610,11 +611,16 @@ Tensor SpConvCache::mapped_table(int log2w, const Tensor& row_map, int shift, i6
   REQ(shift >= 0 && shift < 31, "shift=%d", shift);
   const RowTable& rt = row_table(log2w);
   Tensor t = empty(rt.tbl.sh, I32);
-  const i64 entries = rt.tbl.numel();
-  k_map_table<<<cdiv(entries, 256), 256, 0, stream()>>>(rt.tbl.ptr<uint32_t>(), entries, row_map.ptr<int32_t>(), shift,
-                                                        (uint32_t)std::min<i64>(m, EMPTY), t.ptr<uint32_t>());
-  CK(hipGetLastError());
+  map_table_rows(rt.tbl, row_map, shift, m, t);
   return t;
+}
+
+void map_table_rows(const Tensor& tbl, const Tensor& row_map, int shift, i64 m, Tensor& out) {
+  REQ(out.numel() == tbl.numel(), "mapped table size");
+  const i64 entries = tbl.numel();
+  k_map_table<<<cdiv(entries, 256), 256, 0, stream()>>>(tbl.ptr<uint32_t>(), entries, row_map.ptr<int32_t>(), shift,
+                                                        (uint32_t)std::min<i64>(m, EMPTY), out.ptr<uint32_t>());
+  CK(hipGetLastError());
 }
 
 const std::pair<Tensor, Tensor>& SpConvCache::valid(int B1) {
@@ -761,9 +767,19 @@ __global__ void __launch_bounds__(B) k_halo_build(const uint32_t* __restrict__ n
   for (int d = 1; d < 16; d <<= 1) mask |= (uint32_t)__shfl_xor((int)mask, d, 64);
   if ((tid & 15) == 0) gm[t * (B / 16) + tid / 16] = mask;
   if (tid == 0) {
-    count[t] = min(U, UM);
-    if (bad || U > UM) atomicMax(overflow, 1);
+    count[t] = U > UM ? -1 : U;  // a spill tile: served by the gathering kernel
+    if (bad) atomicMax(&overflow[0], 1);
+    if (U > UM) atomicAdd(&overflow[1], 1);
   }
+}
+
+// Positions of the spill tiles, in tile order: out[j*B + r] = order[tiles[j]*B + r] for positions below n.
+__global__ void k_spill_order(const int32_t* __restrict__ order, const int32_t* __restrict__ tiles, int k, int B, i64 n,
+                              int32_t* __restrict__ out) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (i64)k * B) return;
+  const i64 pos = (i64)tiles[i / B] * B + i % B;
+  if (pos < n) out[i] = order[pos];
 }
 }  // namespace
 
@@ -780,8 +796,8 @@ const SpConvCache::HaloTable& SpConvCache::halo_table(int B, int UM) {
   h.count = empty({tiles}, I32);
   h.idx = empty({tiles * 27 * B / 2}, I32);  // u16 entries
   h.gm = empty({tiles * (B / 16)}, I32);
-  Tensor flag = empty({1}, I32);
-  k_fill_i32<<<1, 64, 0, stream()>>>(flag.ptr<int32_t>(), 1, 0);
+  Tensor flag = empty({2}, I32);  // [0]: the order is not a window order, [1]: spill tiles
+  k_fill_i32<<<1, 64, 0, stream()>>>(flag.ptr<int32_t>(), 2, 0);
   auto go = [&](auto kern) {
     kern<<<(unsigned)tiles, B, 0, stream()>>>(nbr.ptr<uint32_t>(), h.order.ptr<int32_t>(), N, h.rows.ptr<int32_t>(),
                                               h.count.ptr<int32_t>(), (uint16_t*)h.idx.p, h.gm.ptr<uint32_t>(),
@@ -790,6 +806,28 @@ const SpConvCache::HaloTable& SpConvCache::halo_table(int B, int UM) {
   if (B == 256 && UM == 512) go(k_halo_build<256, 512>);
   else REQ(false, "no halo builder for B=%d UM=%d", B, UM);
   CK(hipGetLastError());
-  h.ok = to_host_vec<int32_t>(flag)[0] == 0;  // one host sync per cache and shape
+  const auto fl = to_host_vec<int32_t>(flag);  // one host sync per cache and shape
+  h.ok = fl[0] == 0;
+  if (h.ok && fl[1] > 0) {  // spill tiles: their positions become a row table for the gathering kernel
+    const auto cnt = to_host_vec<int32_t>(h.count);
+    std::vector<int32_t> list;
+    for (i64 t = 0; t < tiles; t++)
+      if (cnt[t] < 0) list.push_back((int32_t)t);
+    REQ((i64)list.size() == fl[1], "spill tiles %zu, flagged %d", list.size(), fl[1]);
+    const int k = (int)list.size();
+    Tensor tl = from_host(list.data(), {k}, I32);
+    const i64 last = list.back();
+    h.spill_n = (i64)k * B - ((last + 1) * B > N ? (last + 1) * B - N : 0);  // only the last tile can be partial
+    h.spill.order = empty({(i64)k * B}, I32);
+    k_spill_order<<<cdiv((i64)k * B, 256), 256, 0, stream()>>>(h.order.ptr<int32_t>(), tl.ptr<int32_t>(), k, B, N,
+                                                               h.spill.order.ptr<int32_t>());
+    const i64 npad = cdiv(h.spill_n, kRowTablePad) * (i64)kRowTablePad;
+    h.spill.tbl = empty({npad, 27}, I32);
+    h.spill.gs = empty({npad}, I32);
+    k_row_table<<<cdiv(npad, 256), 256, 0, stream()>>>(nbr.ptr<uint32_t>(), gray.ptr<int32_t>(),
+                                                            h.spill.order.ptr<int32_t>(), N, h.spill_n, npad,
+                                                            h.spill.tbl.ptr<uint32_t>(), h.spill.gs.ptr<int32_t>());
+    CK(hipGetLastError());
+  }
   return halo.emplace(std::make_pair(B, UM), h).first->second;
 }

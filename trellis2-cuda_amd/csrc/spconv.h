@@ -47,11 +47,14 @@ struct SpConvCache {
   // Halo schedule for the 64-output-channel convs: tiles of B consecutive entries of order = window_order(log2 B)
   // (B-row windows of the input order, gray-sorted inside). Per tile: the distinct neighbour rows it reads
   // (rows[t*UM + u], u < count[t]), each position's 27 neighbours as indices into that list (idx[(t*27 + v)*B + j],
-  // u16; UM = EMPTY, a zero row) and the per-16-position neighbour masks (gm[t*B/16 + g]). ok = false when a tile
-  // reads more than UM distinct rows (its conv then uses the gathering kernel). Built on first use per (B, UM), one
-  // host sync for ok, memoized.
+  // u16; UM = EMPTY, a zero row) and the per-16-position neighbour masks (gm[t*B/16 + g]). A tile that reads more
+  // than UM distinct rows is a spill tile: count[t] = -1 (the halo kernel skips it) and its positions go, in tile
+  // order, into `spill` (a row table of spill_n positions for the gathering kernel). ok = false only when the order
+  // is not a window order. Built on first use per (B, UM), one host sync, memoized.
   struct HaloTable {
     Tensor order, rows, count, idx, gm;
+    RowTable spill;
+    i64 spill_n = 0;
     bool ok = false;
   };
   std::map<std::pair<int, int>, HaloTable> halo;
@@ -137,6 +140,10 @@ void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, 
 // h[i, c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep], rep = Co / (Cin/8), fp32 sum rounded once (bit-identical
 // to the reference). h [m,Co] and x [n,Cin] of one dtype (fp16/bf16); entries of src outside x leave the row.
 void add_skip(Tensor& h, const Tensor& x, const Tensor& src);
+
+// out[i] = row_map[tbl[i]] >> shift for every entry of a neighbour table, EMPTY where tbl[i] is EMPTY or the
+// mapped row is not below m (the row-map form of a tile-order table, for the gathered conv).
+void map_table_rows(const Tensor& tbl, const Tensor& row_map, int shift, i64 m, Tensor& out);
 
 // Child subdivision of a sparse level (reference src/sdec.cu:20-57): children of each parent whose fp16 logit is
 // > 0, in (parent, slot) order, coords (b, 2x+(s&1), 2y+(s>>1&1), 2z+(s>>2&1)), src = parent*8+s.
