@@ -148,6 +148,14 @@ int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, int Co, 
 int spc_subdivide(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
                   int32_t* src, int64_t* m);
 
+/* spc_subdivide without allocating and without waiting: the same children into child_coords int32 [>= 8n, 4] and
+ * src int32 [>= 8n], their count into *m_dev (DEVICE int64). No counterpart in the reference: it is for callers that
+ * cannot allocate device memory or block on the host (code under HIP graph capture, tight serving loops). Its
+ * scratch (per-parent counts and scan sums, about 16 MiB) is a static device array that each GPU holds until the
+ * process ends, so n <= 4194304 (larger n fails with an error) and calls that overlap on one GPU race. */
+int spc_subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
+                          int32_t* src, int64_t* m_dev);
+
 #ifdef __cplusplus
 }
 #endif

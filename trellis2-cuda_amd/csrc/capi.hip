@@ -256,3 +256,8 @@ SPC_API int spc_subdivide(const int32_t* coords, const uint16_t* logits_f16, int
     *m = k;
   });
 }
+
+SPC_API int spc_subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
+                                  int32_t* src, int64_t* m_dev) {
+  return guarded([&] { subdivide_noalloc(coords, logits_f16, n, child_coords, src, m_dev); });
+}

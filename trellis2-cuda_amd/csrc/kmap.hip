@@ -667,6 +667,66 @@ Subdivision subdivide(const Tensor& coords, const Tensor& logits) {
   return o;
 }
 
+// ------------------------------------------------------------------------------------------ subdivision, no allocation
+// The allocation-free variant keeps its one scratch buffer -- the per-parent child counts, scanned in place into
+// output offsets, plus the scan's tile sums -- in a file-scope device array. Every GPU holds its own copy of the
+// array (at its own address) until the process ends; calls on one GPU share it, so calls that overlap on one GPU
+// race. Every word a call reads is written earlier in the same call (the count kernel writes all n + 1 entries),
+// so nothing needs clearing between calls.
+namespace {
+constexpr i64 kNoAllocMaxParents = i64(1) << 22;
+constexpr i64 kNoAllocScratchWords = ((kNoAllocMaxParents + 1 + 63) / 64) * 64 + 2048;  // offsets + tile sums
+__device__ __align__(256) uint32_t scratch[kNoAllocScratchWords];
+
+__global__ void k_store_count(const uint32_t* __restrict__ total, i64* __restrict__ m) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) m[0] = total ? (i64)total[0] : 0;
+}
+
+// Device address of this GPU's copy of `scratch`; looked up once per device (the array's name is only a host-side
+// stand-in, never a device address).
+uint32_t* noalloc_scratch() {
+  static uint32_t* ptr[64] = {};
+  int dev = 0;
+  CK(hipGetDevice(&dev));
+  REQ(dev >= 0 && dev < 64, "device %d", dev);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    CK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    REQ(p != nullptr, "scratch symbol has no device address");
+    ptr[dev] = (uint32_t*)p;
+  }
+  return ptr[dev];
+}
+}  // namespace
+
+i64 subdivide_noalloc_max_parents() { return kNoAllocMaxParents; }
+
+void subdivide_noalloc_init() { (void)noalloc_scratch(); }
+
+void subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, i64 n, int32_t* child_coords, int32_t* src,
+                       i64* m_dev) {
+  REQ(n >= 0 && n <= kNoAllocMaxParents, "subdivide_noalloc: %lld parents, at most %lld", (long long)n,
+      (long long)kNoAllocMaxParents);
+  REQ(m_dev, "m is null");
+  uint32_t* ws = noalloc_scratch();
+  hipStream_t s = stream();
+  if (n == 0) {
+    k_store_count<<<1, 64, 0, s>>>(nullptr, m_dev);
+    CK(hipGetLastError());
+    return;
+  }
+  REQ(coords && logits_f16 && child_coords && src, "null argument");
+  uint32_t* off = ws;                                    // n + 1 offsets
+  uint32_t* part = ws + ((n + 1 + 63) / 64) * 64;        // tile sums of the scan
+  REQ((part - ws) + excl_scan_parts(n + 1) <= kNoAllocScratchWords, "scratch layout");
+  k_c2s_count<<<cdiv(n + 1, 256), 256, 0, s>>>((const uint4*)logits_f16, n, off);
+  excl_scan_u32_ws(off, off, n + 1, nullptr, part);
+  k_store_count<<<1, 64, 0, s>>>(off + n, m_dev);
+  k_c2s_emit<<<cdiv(n, 256), 256, 0, s>>>((const uint4*)logits_f16, (const int4*)coords, off, n, (int4*)child_coords,
+                                          src);
+  CK(hipGetLastError());
+}
+
 // ------------------------------------------------------------------------------------------ halo schedule
 namespace {
 constexpr int kHaloSlots = 1024;  // LDS hash slots per tile (>= 2 * kHaloMax)

@@ -83,13 +83,20 @@ __global__ void __launch_bounds__(ST) k_scan_apply(const uint32_t* __restrict__ 
 }
 }  // namespace
 
+i64 excl_scan_parts(i64 n) { return n <= 0 ? 0 : (n + STILE - 1) / STILE; }
+
+void excl_scan_u32_ws(const uint32_t* in, uint32_t* out, i64 n, uint32_t* total_dev, uint32_t* part) {
+  if (n <= 0) return;
+  i64 nt = excl_scan_parts(n);
+  hipStream_t s = stream();
+  k_scan_reduce<<<(unsigned)nt, ST, 0, s>>>(in, n, part);
+  k_scan_parts<<<1, ST, 0, s>>>(part, nt, total_dev);
+  k_scan_apply<<<(unsigned)nt, ST, 0, s>>>(in, out, n, part);
+  CK(hipGetLastError());
+}
+
 void excl_scan_u32(const uint32_t* in, uint32_t* out, i64 n, uint32_t* total_dev) {
   if (n <= 0) return;
-  i64 nt = (n + STILE - 1) / STILE;
-  Tensor part = empty({nt}, I32);
-  hipStream_t s = stream();
-  k_scan_reduce<<<(unsigned)nt, ST, 0, s>>>(in, n, part.ptr<uint32_t>());
-  k_scan_parts<<<1, ST, 0, s>>>(part.ptr<uint32_t>(), nt, total_dev);
-  k_scan_apply<<<(unsigned)nt, ST, 0, s>>>(in, out, n, part.ptr<uint32_t>());
-  CK(hipGetLastError());
+  Tensor part = empty({excl_scan_parts(n)}, I32);
+  excl_scan_u32_ws(in, out, n, total_dev, part.ptr<uint32_t>());
 }

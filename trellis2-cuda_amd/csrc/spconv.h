@@ -151,3 +151,10 @@ struct Subdivision {
   Tensor coords, src;  // int32 [M,4], int32 [M]
 };
 Subdivision subdivide(const Tensor& coords, const Tensor& logits_f16);
+// The same children written into caller buffers of >= 8n rows, the count into device memory (*m_dev, int64), with no
+// allocation and no host sync: its scratch is a static device array (see kmap.hip), so n <= the maximum below and
+// concurrent calls on one GPU race. init() looks up the array's device address on the current device.
+i64 subdivide_noalloc_max_parents();
+void subdivide_noalloc_init();
+void subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, i64 n, int32_t* child_coords, int32_t* src,
+                       i64* m_dev);

@@ -29,7 +29,7 @@ SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build
            "spc_fdg_quads", "spc_cache_free", "spc_cache_info", "spc_cache_valid", "spc_conv_cfg",
            "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
            "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subm_conv_skip",
-           "spc_subdivide")
+           "spc_subdivide", "spc_subdivide_noalloc")
 
 _lib = None
 
@@ -65,6 +65,7 @@ def load_library():
     L.spc_convnext_mlp.argtypes = [P, P, P, P, ctypes.c_float, P, P, P, P, I, I, I64, I, P]
     L.spc_subm_conv_skip.argtypes = [P, P, P, I, I, I, P, I64, I, P, I64, I, I, P, P]
     L.spc_subdivide.argtypes = [P, P, I64, P, P, ctypes.POINTER(I64)]
+    L.spc_subdivide_noalloc.argtypes = [P, P, I64, P, P, P]
     for name in SYMBOLS:
         if name != "spc_last_error":
             getattr(L, name).restype = I
