@@ -141,6 +141,17 @@ int spc_subm_conv_skip(const void* x, const void* w, const void* b, int dtype, i
  * Replaces: k_add_skip (src/sdec.cu:38-43, launched at :84). */
 int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, int Co, int64_t n, int Cin, int dtype);
 
+/* The reference's fp16 conv under a given tile choice (B1, BK, S) -- e.g. spc_conv_cfg_autotune's -- rounding
+ * included: S == 1 is spc_subm_conv_fused with SPC_EPI_F16_COMPAT; S > 1 computes fp32 partials per split (each split
+ * takes its share of every B1-row block's K chunks, the fp32 bias goes into split 0) and sums them with four
+ * interleaved accumulators before one fp16 rounding; act (SPC_ACT_NONE/SPC_ACT_SILU) and residual (or NULL) then
+ * round as the reference's separate passes. x, w, b, residual, out: fp16. B1 and BK multiples of 32, Ci % BK == 0,
+ * Co % 32 == 0, 1 <= S <= 64.
+ * Replaces: subm_conv's k_spconv + k_splitk_sum path and its act_ / add_ passes (src/spconv.cu:90-175,
+ * src/ops.cu:79-82,105-113). */
+int spc_subm_conv_replay(const void* x, const void* w, const void* b, const void* residual, int act, int64_t N, int Ci,
+                         int Co, int B1, int BK, int S, spc_cache* c, void* out);
+
 /* Child subdivision (c2s): children of each parent whose fp16 logit (logits [n,8]) is > 0, in (parent, slot)
  * order; child_coords int32 [>= 8n, 4] and src int32 [>= 8n] receive the children, *m (host) their count
  * (the call waits for the stream, as the reference does at src/sdec.cu:52).

@@ -242,6 +242,18 @@ SPC_API int spc_subm_conv(const void* x, const void* w, const void* b, int dtype
   return spc_subm_conv_fused(x, w, b, nullptr, dtype, b_dtype, SPC_F32, dtype, SPC_ACT_NONE, N, Ci, Co, c, out);
 }
 
+SPC_API int spc_subm_conv_replay(const void* x, const void* w, const void* b, const void* residual, int act, int64_t N,
+                                 int Ci, int Co, int B1, int BK, int S, spc_cache* c, void* out) {
+  return guarded([&] {
+    REQ(c && x && w && out, "null argument");
+    Tensor tx = borrow(x, {N, Ci}, F16), tw = borrow(w, {Co, 27, Ci}, F16), to = borrow(out, {N, Co}, F16);
+    Tensor tb, tr;
+    if (b) tb = borrow(b, {Co}, F16);
+    if (residual) tr = borrow(residual, {N, Co}, F16);
+    subm_conv_replay(tx, tw, b ? &tb : nullptr, residual ? &tr : nullptr, act, SpConvCfg{B1, BK, S}, c->c, to);
+  });
+}
+
 SPC_API int spc_subdivide(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
                           int32_t* src, int64_t* m) {
   return guarded([&] {

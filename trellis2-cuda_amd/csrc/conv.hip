@@ -301,6 +301,7 @@ struct Epi {
   __amdgpu_buffer_rsrc_t out, res;
   int out_dt, res_dt;  // res_dt < 0: no residual
   bool silu;
+  bool compat;  // EPI_F16_COMPAT: the reference's fp16 rounding sequence (fp16 out, bias and residual)
 };
 __device__ __forceinline__ Epi make_epi(const ConvArgs& a) {
   Epi e;
@@ -308,7 +309,8 @@ __device__ __forceinline__ Epi make_epi(const ConvArgs& a) {
   e.res = make_rsrc(a.res, a.res_bytes);
   e.out_dt = a.out_dt;
   e.res_dt = a.res ? a.res_dt : -1;
-  e.silu = a.act == ACT_SILU;  // the tiled kernels never see EPI_F16_COMPAT (dispatch sends it to k_conv)
+  e.silu = (a.act & ~EPI_F16_COMPAT) == ACT_SILU;
+  e.compat = (a.act & EPI_F16_COMPAT) != 0;
   return e;
 }
 
@@ -327,6 +329,20 @@ __device__ __forceinline__ void load_res8(const Epi& e, uint32_t o, bool ok, u32
 // out[o .. o+8) = act(v + bias) [+ residual r], one rounding to the output dtype
 __device__ __forceinline__ void store_row8(const Epi& e, uint32_t o, bool ok, float (&v)[8], const float (&bias8)[8],
                                            const u32x4 (&r)[2]) {
+  if (e.compat) {  // f16(f16(acc) + b), then f16(silu), then f16(y + residual); every value is an fp16 from here
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      float y = f16r(f16r(v[q]) + bias8[q]);
+      if (e.silu) y = f16r(silu_ieee(y));
+      if (e.res_dt == F16) y = f16r(y + f16_to_f32((uint16_t)(r[0][q >> 1] >> ((q & 1) * 16))));
+      v[q] = y;
+    }
+    u32x4 w;
+#pragma unroll
+    for (int q = 0; q < 4; q++) w[q] = pack2<false>(v[2 * q], v[2 * q + 1]);
+    __builtin_amdgcn_raw_buffer_store_b128(w, e.out, ok ? o * 2u : kOutOfRange, 0, 0);
+    return;
+  }
 #pragma unroll
   for (int q = 0; q < 8; q++) v[q] += bias8[q];
   if (e.silu) {
@@ -1925,11 +1941,9 @@ void launch(ConvArgs a) {
 
 template <bool F16>
 void dispatch(const SpConvCfg& cfg, ConvArgs a) {
-  // The fp16-compatible epilogue runs in the generic kernel only: its longer rounding sequence (IEEE quotient,
-  // accurate exp) would cost the tuned kernels registers in their epilogues.
-  const bool compat = a.act & EPI_F16_COMPAT;
+  // The fp16-compatible epilogue (EPI_F16_COMPAT) runs in every kernel: store_row8 applies it.
   if (a.hrows) return launch_halo<F16, 2>(a);
-  if (!compat && a.Co == 64 && a.Ci <= 128) {
+  if (a.Co == 64 && a.Ci <= 128) {
     switch (a.Ci / 32) {
       case 1: return launch_narrow<F16, 1, 4>(a);
       case 2: return launch_narrow<F16, 2, 4>(a);
@@ -1938,9 +1952,9 @@ void dispatch(const SpConvCfg& cfg, ConvArgs a) {
     }
   }
   // Fixed tiles per channel width (no autotune): BM = 128 sorted rows per tile.
-  if (!compat && a.Co % 256 == 0 && a.Ci % 64 == 0 && w256_enabled()) return launch_w256<F16>(a);
-  if (!compat && cfg.BK == 64 && a.Co % 256 == 0) return launch_wide_dma<F16>(a);
-  if (!compat && cfg.BK == 64 && a.Co % 128 == 0) return launch_wide<F16, 2, 128>(a);
+  if (a.Co % 256 == 0 && a.Ci % 64 == 0 && w256_enabled()) return launch_w256<F16>(a);
+  if (cfg.BK == 64 && a.Co % 256 == 0) return launch_wide_dma<F16>(a);
+  if (cfg.BK == 64 && a.Co % 128 == 0) return launch_wide<F16, 2, 128>(a);
   if (a.Co % 128 == 0) {
     if (cfg.BK == 64) launch<F16, 128, 128, 2, 2, 64>(a);
     else launch<F16, 128, 128, 2, 2, 32>(a);
@@ -1960,7 +1974,8 @@ SpConvCfg spconv_cfg(int N, int Ci, int Co) {
 // The kernels that read their tiles' neighbour rows from the tile-order table (narrow, 256-channel wide) can read
 // them through a row map instead; the others get the gathered rows materialized.
 bool reads_row_table(const SpConvCfg& cfg, int Ci, int Co, int act) {
-  return !(act & EPI_F16_COMPAT) && ((Co == 64 && Ci <= 128) || (cfg.BK == 64 && Co % 256 == 0));
+  (void)act;
+  return (Co == 64 && Ci <= 128) || (cfg.BK == 64 && Co % 256 == 0);
 }
 
 __global__ void k_gather_rows(const u32x4* __restrict__ x, i64 m, int units, const int32_t* __restrict__ row_map,
@@ -2054,9 +2069,8 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   a.act = act;
   Tensor wpack, mtbl;
   REQ(!row_map || reads_row_table(cfg, Ci, Co, act), "row map with a kernel that reads nbr directly");
-  const bool compat = act & EPI_F16_COMPAT;
   const SpConvCache::HaloTable* ht = nullptr;
-  if (!compat && Co == 64 && Ci == 64 && halo_enabled()) {
+  if (Co == 64 && Ci == 64 && halo_enabled()) {
     ht = &c.halo_table(HaloShape<2>::B, HaloShape<2>::UM);
     if (!ht->ok) ht = nullptr;
   }
@@ -2085,7 +2099,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       a.res_dt = skip->x->dt;
       a.res_bytes = a.skip_bytes;
     }
-  } else if (!compat && Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, spatial row order
+  } else if (Co == 64 && Ci <= 128) {  // narrow kernel: weights in 16x16x32 operand order, spatial row order
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<dim3(Ci / 32, Co / 16, 27), 64, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
@@ -2095,7 +2109,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
     a.gs = rt.gs.ptr<int32_t>();
     a.tbl_bytes = (uint32_t)rt.tbl.bytes();
-  } else if (!compat && Co % 256 == 0 && Ci % 64 == 0 && w256_enabled()) {  // 256 x 256 tiles: 4 KB weight blocks
+  } else if (Co % 256 == 0 && Ci % 64 == 0 && w256_enabled()) {  // 256 x 256 tiles: 4 KB weight blocks
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w256<<<dim3(Ci / 64, 27, Co / 32), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Ci);
     a.w = wpack.ptr<uint16_t>();
@@ -2105,7 +2119,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     a.gs = rt.gs.ptr<int32_t>();
     a.tbl_bytes = (uint32_t)rt.tbl.bytes();
     a.tsched = c.tile_schedule(-1, 256).ptr<int32_t>();
-  } else if (!compat && cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
+  } else if (cfg.BK == 64 && Co % 128 == 0) {  // wide kernels read the 32x32x16-ordered weight copy
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w<<<dim3(Ci / 64 * 2, 27, Co / 64), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();

@@ -107,6 +107,13 @@ constexpr int EPI_F16_COMPAT = 256;
 void subm_conv_fused(const Tensor& x, const Tensor& w, const Tensor* b, const Tensor* residual, int act,
                      SpConvCache& c, Tensor& out);
 
+// The reference's fp16 conv under a replayed FlexGEMM tile choice (spconv_cfg_autotune), rounding included: S == 1
+// is subm_conv_fused with EPI_F16_COMPAT; S > 1 writes fp32 partials per split (the split's share of each B1
+// block's K chunks, fp32 bias in split 0) and sums them with four interleaved accumulators before the one fp16
+// rounding (src/spconv.cu:98-99,144-157), then act / residual as the reference's separate fp16 passes. fp16 only.
+void subm_conv_replay(const Tensor& x, const Tensor& w, const Tensor* b, const Tensor* residual, int act,
+                      const SpConvCfg& cfg, SpConvCache& c, Tensor& out);
+
 // Conv of gathered rows without materializing them: out = subm_conv_fused(x_src[row_map >> shift], ...).
 // x_src [M,Ci]; row_map int32 [N] (N = the cache's rows), e.g. the c2s parent map (src, shift 3), so a decoder's
 // upsample block (reference src/sdec.cu:34-43 k_gather_rows then the conv at :70-87) reads the parent rows

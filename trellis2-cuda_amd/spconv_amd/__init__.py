@@ -29,7 +29,7 @@ SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build
            "spc_fdg_quads", "spc_cache_free", "spc_cache_info", "spc_cache_valid", "spc_conv_cfg",
            "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
            "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subm_conv_skip",
-           "spc_subdivide", "spc_subdivide_noalloc")
+           "spc_subdivide", "spc_subdivide_noalloc", "spc_subm_conv_replay")
 
 _lib = None
 
@@ -66,6 +66,7 @@ def load_library():
     L.spc_subm_conv_skip.argtypes = [P, P, P, I, I, I, P, I64, I, P, I64, I, I, P, P]
     L.spc_subdivide.argtypes = [P, P, I64, P, P, ctypes.POINTER(I64)]
     L.spc_subdivide_noalloc.argtypes = [P, P, I64, P, P, P]
+    L.spc_subm_conv_replay.argtypes = [P, P, P, P, I, I64, I, I, I, I, I, P, P]
     for name in SYMBOLS:
         if name != "spc_last_error":
             getattr(L, name).restype = I
@@ -335,6 +336,19 @@ def subm_conv(x, w, b, cache: SpConvCache):
     y = torch.empty((N, Co), dtype=x.dtype, device=x.device)
     _check(load_library().spc_subm_conv(_ptr(x), _ptr(w), _ptr(b), _dt(x), _dt(b) if b is not None else F32,
                                         N, Ci, Co, cache._h, _ptr(y)))
+    return y
+
+
+def subm_conv_replay(x, w, b, cache, cfg, residual=None, act=ACT_NONE):
+    """The reference's fp16 conv under the tile choice cfg = (B1, BK, S), rounding included (split-K partials summed
+    with four interleaved accumulators when S > 1). fp16 x, w, b, residual; returns fp16 [N, Co]."""
+    torch = _torch()
+    N, Ci = x.shape
+    Co = w.shape[0]
+    y = torch.empty((N, Co), dtype=torch.float16, device=x.device)
+    B1, BK, S = cfg
+    _check(load_library().spc_subm_conv_replay(_ptr(x), _ptr(w), _ptr(b), _ptr(residual), act, N, Ci, Co, B1, BK, S,
+                                               cache._h, _ptr(y)))
     return y
 
 
