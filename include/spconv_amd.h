@@ -117,7 +117,8 @@ int spc_gather_ln_act(const void* x_src, int64_t M, int C, const int32_t* row_ma
 /* ConvNeXt tail in one pass: y = x + W2 silu(W1 (LayerNorm(h) * gamma + beta) + b1) + b2 per row, fp32 statistics
  * and accumulation, the hidden activations rounded to `dtype` between the two products, one rounding of y.
  * h, x, y [N,C], w1 [4C,C], w2 [C,4C] (torch Linear layout): `dtype` (SPC_F16/SPC_BF16), 16-byte aligned;
- * gamma, beta, b2 [C] and b1 [4C]: `param_dtype` or NULL (gamma 1, others 0); C = 64, 128 or 256.
+ * gamma, beta, b2 [C] and b1 [4C]: `param_dtype` or NULL (gamma 1, others 0); C = 64, 128 or 256 (one fused pass)
+ * or 512, 1024 (LayerNorm pass, then two GEMM passes with the bias/SiLU and bias/residual epilogues).
  * y may alias h or x.
  * Replaces: the tail of SDecoder::convnext after its conv -- layer_norm, linear, act_ SILU, linear, add_
  * (src/sdec.cu:60-66, src/ops.cu:30-75, src/gemm.cu:24-63). */

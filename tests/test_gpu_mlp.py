@@ -52,7 +52,7 @@ def check(y, args, eps, dt, what):
     assert r_em <= 2e-3 and mx <= 3e-2 and r_32 <= 1e-2, what
 
 
-@pytest.mark.parametrize("C", [64, 128, 256])
+@pytest.mark.parametrize("C", [64, 128, 256, 512, 1024])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_convnext_mlp(gpu, C, dt):
     print(f"mlp case C={C} dt={dt}", flush=True)
@@ -62,11 +62,11 @@ def test_convnext_mlp(gpu, C, dt):
         check(y, args, 1e-6, dt, f"C={C} N={N} {dt} params {pdt}")
 
 
-@pytest.mark.parametrize("C", [64, 128])
+@pytest.mark.parametrize("C", [64, 128, 512])
 def test_convnext_mlp_many_tiles_in_place(gpu, C):
-    """More row tiles than workgroups (the persistent loop and, for C = 128, the weight stream across tiles), no
-    affine and no biases, output written over h."""
-    N = 70001 if C == 64 else 140001
+    """More row tiles than workgroups (the persistent loop and, for C = 128, the weight stream across tiles; for
+    C = 512 the three-pass form), no affine and no biases, output written over h."""
+    N = {64: 70001, 128: 140001, 512: 20001}[C]
     print(f"mlp many-tiles case C={C} N={N}", flush=True)
     h, x, _, _, w1, _, w2, _ = make(N, C, torch.bfloat16, torch.float32, 5)
     hg = h.to(gpu)
@@ -85,3 +85,8 @@ def test_convnext_mlp_errors(gpu):
     w1 = torch.zeros((256, 64), dtype=torch.bfloat16, device=gpu)
     w2 = torch.zeros((64, 256), dtype=torch.bfloat16, device=gpu)
     assert sp.convnext_mlp(e, e, None, None, w1, None, w2, None).shape == (0, 64)
+    h = torch.zeros((10, 384), dtype=torch.bfloat16, device=gpu)  # C = 384: neither form
+    w1 = torch.zeros((1536, 384), dtype=torch.bfloat16, device=gpu)
+    w2 = torch.zeros((384, 1536), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="512, 1024"):
+        sp.convnext_mlp(h, h, None, None, w1, None, w2, None)

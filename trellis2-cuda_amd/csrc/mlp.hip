@@ -303,6 +303,101 @@ void launch_mlp(const Tensor& h, const Tensor& x, const Tensor& w1, const Tensor
       h.ptr<uint16_t>(), x.ptr<uint16_t>(), y.ptr<uint16_t>(), (const u32x4*)wp.p, params.ptr<float>(), eps, n, tiles,
       (uint32_t)h.bytes(), (uint32_t)x.bytes(), (uint32_t)y.bytes());
 }
+
+// Row-block GEMM with the tail's epilogues, for widths whose fused tile does not fit in registers (C = 512, 1024:
+// the coarse decoder levels, few rows): Y[m, n] = act(A[m, :] · B[n, :] + bias[n]) [+ R[m, n]], one rounding to the
+// operand type. A [M,K], B [N,K] (torch Linear weight layout), R and Y [M,N], all one 16-bit dtype; N % 128 == 0,
+// K % 32 == 0. Workgroup = 128 x 128 tile, 4 wavefronts of 64 x 64 (2 x 2 v_mfma_f32_32x32x16 tiles), K in stages
+// of 32 through double-buffered LDS (row stride 40 halves); rows past M load zeros and store nothing.
+template <bool F16>
+__global__ void __launch_bounds__(256) k_gemm_nt(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                                 const float* __restrict__ bias, const uint16_t* __restrict__ R,
+                                                 uint16_t* __restrict__ Y, int M, int N, int K, int act) {
+  constexpr int BM = 128, BN = 128, BK = 32, LS = BK + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LS], Bs[2][BN * LS];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv & 1, wn = wv >> 1;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  // stage loads: 128 rows x 32 halves = 512 units of 16 bytes per operand, 2 per thread
+  u32x4 ra[2], rb[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int u = tid + j * 256, r = u >> 2, c = (u & 3) * 8;
+      ra[j] = m0 + r < M ? *(const u32x4*)(A + (i64)(m0 + r) * K + k0 + c) : u32x4{0, 0, 0, 0};
+      rb[j] = *(const u32x4*)(B + (i64)(n0 + r) * K + k0 + c);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int u = tid + j * 256, r = u >> 2, c = (u & 3) * 8;
+      *(u32x4*)&As[buf][r * LS + c] = ra[j];
+      *(u32x4*)&Bs[buf][r * LS + c] = rb[j];
+    }
+  };
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+  const int nst = K / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int st = 0; st < nst; st++) {
+    const int buf = st & 1;
+    if (st + 1 < nst) gload((st + 1) * BK);
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 16) {
+      u32x4 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        a[i] = *(const u32x4*)&As[buf][(wm * 64 + i * 32 + (lane & 31)) * LS + ks + (lane >> 5) * 8];
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        b[j] = *(const u32x4*)&Bs[buf][(wn * 64 + j * 32 + (lane & 31)) * LS + ks + (lane >> 5) * 8];
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = mfma32<F16>(a[i], b[j], acc[i][j]);
+    }
+    if (st + 1 < nst) sstore(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+    const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int row = m0 + wm * 64 + i * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
+        if (row >= M) continue;
+        float v = acc[i][j][e] + bv;
+        if (act == ACT_SILU) v = v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+        const i64 o = (i64)row * N + col;
+        if (R) {
+          const uint16_t r = R[o];
+          v += F16 ? (float)__builtin_bit_cast(_Float16, r) : __uint_as_float((uint32_t)r << 16);
+        }
+        Y[o] = F16 ? __builtin_bit_cast(uint16_t, (_Float16)v)
+                   : __builtin_bit_cast(uint16_t, (__bf16)v);
+      }
+  }
+}
+
+template <bool F16>
+void gemm_nt(const Tensor& a, const Tensor& b, const float* bias, const Tensor* r, int act, Tensor& y) {
+  const int M = (int)a.size(0), K = (int)a.size(1), N = (int)b.size(0);
+  REQ(N % 128 == 0 && K % 32 == 0, "gemm N=%d K=%d", N, K);
+  if (M == 0) return;
+  k_gemm_nt<F16><<<dim3(cdiv(M, 128), N / 128), 256, 0, stream()>>>(
+      a.ptr<uint16_t>(), b.ptr<uint16_t>(), bias, r ? r->ptr<uint16_t>() : nullptr, y.ptr<uint16_t>(), M, N, K, act);
+  CK(hipGetLastError());
+}
 }  // namespace
 
 void convnext_mlp(const Tensor& h, const Tensor& x, const Tensor* gamma, const Tensor* beta, float eps, const Tensor& w1,
@@ -310,7 +405,8 @@ void convnext_mlp(const Tensor& h, const Tensor& x, const Tensor* gamma, const T
   REQ(h.dim() == 2 && (h.dt == BF16 || h.dt == F16), "h must be bf16/fp16 [N,C]");
   const i64 n = h.size(0);
   const int C = (int)h.size(1);
-  REQ(C == 64 || C == 128 || C == 256, "C=%d: the fused tail supports C = 64, 128, 256", C);
+  REQ(C == 64 || C == 128 || C == 256 || C == 512 || C == 1024,
+      "C=%d: the tail supports C = 64, 128, 256 (fused) and 512, 1024 (three passes)", C);
   REQ(x.dt == h.dt && x.dim() == 2 && x.size(0) == n && x.size(1) == C, "x must match h");
   REQ(y.dt == h.dt && y.dim() == 2 && y.size(0) == n && y.size(1) == C, "y must match h");
   REQ(w1.dt == h.dt && w1.dim() == 2 && w1.size(0) == 4 * C && w1.size(1) == C, "w1 must be [4C, C] of h's dtype");
@@ -331,6 +427,22 @@ void convnext_mlp(const Tensor& h, const Tensor& x, const Tensor* gamma, const T
   conv(b1, 2 * C, 4 * C, 0.f);
   conv(b2, 6 * C, C, 0.f);
   const bool f16 = h.dt == F16;
+  if (C >= 512) {
+    // coarse levels: LayerNorm + affine (one pass), then the two products with their epilogues (hidden rounded to
+    // the operand type, as in the fused kernel); the residual is read and y written by the same thread, so y may
+    // alias x, and h is consumed before y is written
+    Tensor g = borrow(pp, {C}, F32), bt = borrow(pp + C, {C}, F32);
+    Tensor a = empty({n, C}, h.dt), hid = empty({n, 4 * (i64)C}, h.dt);
+    gather_ln_act(h, nullptr, 0, &g, &bt, eps, ACT_NONE, a);
+    if (f16) {
+      gemm_nt<true>(a, w1, pp + 2 * C, nullptr, ACT_SILU, hid);
+      gemm_nt<true>(hid, w2, pp + 6 * C, &x, ACT_NONE, y);
+    } else {
+      gemm_nt<false>(a, w1, pp + 2 * C, nullptr, ACT_SILU, hid);
+      gemm_nt<false>(hid, w2, pp + 6 * C, &x, ACT_NONE, y);
+    }
+    return;
+  }
   // measured on the MI355X (2.2 M / 0.8 M / 0.4 M rows): two 32-row blocks per wavefront halve the LDS weight
   // reads at C = 128; at C = 256 the residual is loaded in the epilogue to stay clear of spills
   if (C == 64) f16 ? launch_mlp<true, 64, 1, 4, true>(h, x, w1, w2, params, eps, y) : launch_mlp<false, 64, 1, 4, true>(h, x, w1, w2, params, eps, y);

@@ -131,8 +131,8 @@ void gather_ln_act(const Tensor& x_src, const Tensor* row_map, int shift, const 
 // ConvNeXt tail of the decoder in one pass (reference SDecoder::convnext after its conv, src/sdec.cu:60-66):
 // y = x + W2 silu(W1 (LayerNorm(h) * gamma + beta) + b1) + b2 per row, LayerNorm eps as given, fp32 accumulation,
 // hidden activations rounded to h's dtype between the two products. h, x, y [N,C] and w1 [4C,C], w2 [C,4C] of one
-// dtype (fp16/bf16); gamma, beta, b2 [C] and b1 [4C] of any float dtype or null; C = 64, 128 or 256. y may alias h
-// or x.
+// dtype (fp16/bf16); gamma, beta, b2 [C] and b1 [4C] of any float dtype or null; C = 64, 128 or 256 in one pass,
+// C = 512 or 1024 (the coarse levels) as LayerNorm + two GEMMs with fused epilogues. y may alias h or x.
 void convnext_mlp(const Tensor& h, const Tensor& x, const Tensor* gamma, const Tensor* beta, float eps, const Tensor& w1,
                   const Tensor* b1, const Tensor& w2, const Tensor* b2, Tensor& y);
 
