@@ -59,6 +59,20 @@ int spc_cache_lookup(const spc_cache* c, const int32_t* query, int64_t m, int32_
  * Replaces: k_fdg_quads and its hash (src/mesh.cu:7-19, 36-45, 54-62). */
 int spc_fdg_quads(const spc_cache* c, const float* h, int32_t* quad, int32_t* ok);
 
+/* Trilinear sample map of L points grid f32 [L,3] (continuous voxel coordinates: voxel i spans [i, i+1)) in batch
+ * `batch` of a cache built with SPC_KEEP_HASH: nb u32 [L,8] = the rows of the 8 voxels around p - 0.5 (corner
+ * v = dx*4 + dy*2 + dz; SPC_EMPTY when absent or off-grid), wt f32 [L,8] = their trilinear weights (0 for EMPTY
+ * corners). flags: SPC_GS_NORMALIZE divides the present weights by their sum.
+ * Replaces: the bake's FlexGEMM hashmap_build_grid_sample_3d_trilinear_neighbor_map_weight and its voxel hash
+ * (src/glb.cu:547-550). */
+enum { SPC_GS_NORMALIZE = 1 };
+int spc_grid_sample_map(const spc_cache* c, const float* grid, int64_t L, int batch, int flags, uint32_t* nb,
+                        float* wt);
+
+/* y f32 [L,C] = sum over v of x[nb[i,v]] * wt[i,v] (x f32 [M,C]; fused multiply-adds in v order, SPC_EMPTY reads 0).
+ * Replaces: k_wsum (src/glb.cu:456-465, launched at :552). */
+int spc_grid_sample_sum(const float* x, int64_t M, int C, const uint32_t* nb, const float* wt, int64_t L, float* y);
+
 /* Release a cache (its device buffers are freed in stream order). */
 int spc_cache_free(spc_cache* c);
 

@@ -207,3 +207,70 @@ def test_fdg_quads(gpu, name, R):
     np.testing.assert_array_equal(ok, ook)
     assert ok.sum() > 0
     np.testing.assert_array_equal(quad.cpu().numpy()[ok == 1], oq[ook == 1])
+
+
+def dense_volume(c, attrs, X, Y, Z):
+    """attrs of the sparse voxels scattered into a zero volume laid out for torch's 5-D grid_sample: [1, C, Z, Y, X]
+    (grid's last dimension is (x, y, z) -> (W, H, D))."""
+    vol = torch.zeros((1, attrs.shape[1], Z, Y, X), dtype=torch.float64)
+    ci = torch.from_numpy(c.astype(np.int64))
+    vol[0, :, ci[:, 3], ci[:, 2], ci[:, 1]] = attrs.double().T
+    return vol
+
+
+def torch_sample(vol, pts, X, Y, Z):
+    """torch.nn.functional.grid_sample, trilinear, align_corners=False, zero padding: continuous voxel coordinate p
+    (voxel i spans [i, i+1)) normalizes to 2p/size - 1."""
+    size = torch.tensor([X, Y, Z], dtype=torch.float64)
+    g = (2 * pts.double() / size - 1).view(1, 1, 1, -1, 3)
+    return torch.nn.functional.grid_sample(vol, g, mode="bilinear", padding_mode="zeros", align_corners=False)[
+        0, :, 0, 0, :].T
+
+
+@pytest.mark.parametrize("name", ["c1", "dense"])
+def test_grid_sample(gpu, name):
+    """The bake's trilinear sample map + weighted sum on the kept hash, against torch's grid_sample on the dense
+    volume the sparse attributes are scattered into (absent voxels read zero there, as EMPTY corners do here): points
+    inside, on voxel centres and faces, and past the grid edge. Rows bit-exact against dictionary lookups of the 8
+    corners; weights sum to 1 where all corners exist; the normalized form divides by the present weights' sum."""
+    if name == "c1":
+        c = coords("c1")
+        X = Y = Z = 32
+    else:
+        g = np.stack(np.meshgrid(np.arange(6), np.arange(5), np.arange(7), indexing="ij"), -1).reshape(-1, 3)
+        c = np.concatenate([np.zeros((len(g), 1), np.int64), g], 1).astype(np.int32)
+        X, Y, Z = 6, 5, 7
+    rng = np.random.default_rng(3)
+    L = 4000
+    pts = rng.uniform(-1.0, [X + 1, Y + 1, Z + 1], size=(L, 3)).astype(np.float32)
+    pts[:200] = c[rng.integers(0, len(c), 200), 1:] + 0.5  # voxel centres: one corner with weight 1
+    pts[200:300, 0] = np.floor(pts[200:300, 0]) + 0.5      # on a centre plane along x
+    attrs = torch.from_numpy(rng.standard_normal((len(c), 6)).astype(np.float32))
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu), X, Y, Z, keep_hash=True)
+    tp = torch.from_numpy(pts).to(gpu)
+    nb, wt = sp.grid_sample_map(cache, tp)
+    y = sp.grid_sample_sum(attrs.to(gpu), nb, wt).cpu()
+    ref = torch_sample(dense_volume(c, attrs, X, Y, Z), torch.from_numpy(pts), X, Y, Z)
+    assert torch.allclose(y.double(), ref, atol=2e-5, rtol=1e-5), float((y.double() - ref).abs().max())
+    # rows: dictionary lookups of the corners of floor(p - 0.5)
+    d = {tuple(r[1:]): i for i, r in enumerate(c)}
+    base = np.floor(pts.astype(np.float64) - 0.5).astype(np.int64)
+    exp = np.full((L, 8), -1, np.int64)
+    for v in range(8):
+        off = np.array([v >> 2, (v >> 1) & 1, v & 1])
+        q = base + off
+        exp[:, v] = [d.get(tuple(p), -1) for p in q]
+    nbh, wth = nb.cpu().numpy(), wt.cpu().numpy()
+    np.testing.assert_array_equal(nbh, exp)
+    assert np.all(wth[exp < 0] == 0)
+    full = (exp >= 0).all(1)
+    assert np.allclose(wth[full].sum(1), 1.0, atol=1e-6)
+    assert np.all(wth[:200].max(1) == 1.0)  # centres
+    nb2, wt2 = sp.grid_sample_map(cache, tp, normalize=True)
+    assert torch.equal(nb2, nb)
+    s = wth.sum(1, keepdims=True)
+    some = s[:, 0] > 0
+    assert np.allclose(wt2.cpu().numpy()[some], wth[some] / s[some], rtol=1e-6, atol=1e-7)
+    # another batch index finds nothing
+    nb3, wt3 = sp.grid_sample_map(cache, tp, batch=1)
+    assert bool((nb3 == -1).all()) and bool((wt3 == 0).all())

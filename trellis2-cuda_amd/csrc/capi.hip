@@ -254,6 +254,27 @@ SPC_API int spc_subm_conv_replay(const void* x, const void* w, const void* b, co
   });
 }
 
+SPC_API int spc_grid_sample_map(const spc_cache* c, const float* grid, int64_t L, int batch, int flags, uint32_t* nb,
+                                float* wt) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    REQ(L >= 0 && (L == 0 || (grid && nb && wt)), "null argument or L < 0");
+    REQ((flags & ~SPC_GS_NORMALIZE) == 0, "unknown flags %d", flags);
+    Tensor tn = borrow(nb, {L, 8}, I32), tw = borrow(wt, {L, 8}, F32);
+    grid_sample_map(c->c, borrow(grid, {L, 3}, F32), batch, (flags & SPC_GS_NORMALIZE) != 0, tn, tw);
+  });
+}
+
+SPC_API int spc_grid_sample_sum(const float* x, int64_t M, int C, const uint32_t* nb, const float* wt, int64_t L,
+                                float* y) {
+  return guarded([&] {
+    REQ(M >= 0 && L >= 0 && C >= 0, "sizes");
+    REQ(L == 0 || C == 0 || (x && nb && wt && y), "null argument");
+    Tensor ty = borrow(y, {L, C}, F32);
+    grid_sample_sum(borrow(x, {M, C}, F32), borrow(nb, {L, 8}, I32), borrow(wt, {L, 8}, F32), ty);
+  });
+}
+
 SPC_API int spc_subdivide(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
                           int32_t* src, int64_t* m) {
   return guarded([&] {

@@ -418,6 +418,70 @@ __global__ void __launch_bounds__(256) k_fdg_quads(const uint32_t* __restrict__ 
   ok[e] = g;
   if (g) quad[e] = make_int4(r[0], r[1], r[2], r[3]);
 }
+
+// Trilinear sample map (the bake's grid-sample neighbour map + weights): a point p (continuous voxel coordinates,
+// voxel i spans [i, i+1) with its centre at i + 0.5) reads the 8 voxels around u = p - 0.5: corner v = dx*4 + dy*2 +
+// dz of base floor(u), weight ((dx ? fx : 1-fx) * (dy ? fy : 1-fy)) * (dz ? fz : 1-fz), f = u - floor(u). Absent or
+// off-grid corners: EMPTY with weight 0; with `normalize` the present weights are divided by their sum.
+__global__ void __launch_bounds__(256) k_grid_sample_map(const float* __restrict__ grid, i64 L, int b, int W, int H,
+                                                         int D, const ulonglong2* __restrict__ t, uint32_t mask0,
+                                                         const uint32_t* __restrict__ maskp,
+                                                         const uint32_t* __restrict__ bricks, bool normalize,
+                                                         uint32_t* __restrict__ nb, float* __restrict__ wt) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= L) return;
+  const float px = grid[i * 3], py = grid[i * 3 + 1], pz = grid[i * 3 + 2];
+  uint32_t r[8];
+  float w[8];
+  const bool fin = isfinite(px) && isfinite(py) && isfinite(pz) && fabsf(px) < 1e9f && fabsf(py) < 1e9f &&
+                   fabsf(pz) < 1e9f;
+  const float ux = px - 0.5f, uy = py - 0.5f, uz = pz - 0.5f;
+  const float bx = floorf(ux), by = floorf(uy), bz = floorf(uz);
+  const float fx = ux - bx, fy = uy - by, fz = uz - bz;
+  const int x0 = fin ? (int)bx : 0, y0 = fin ? (int)by : 0, z0 = fin ? (int)bz : 0;
+  const uint32_t mask = maskp ? *maskp : mask0;
+  float sum = 0.f;
+#pragma unroll
+  for (int v = 0; v < 8; v++) {
+    const int dx = v >> 2, dy = (v >> 1) & 1, dz = v & 1;
+    const int x = x0 + dx, y = y0 + dy, z = z0 + dz;
+    uint32_t row = EMPTY;
+    if (fin && t && b >= 0 && x >= 0 && y >= 0 && z >= 0 && x < W && y < H && z < D) {
+      const uint32_t id = brick_find(t, brick_key(b, x, y, z, (W + 3) >> 2, (H + 3) >> 2, (D + 3) >> 2), mask);
+      if (id != EMPTY) row = bricks[(i64)id * 64 + brick_local(x, y, z)];
+    }
+    r[v] = row;
+    w[v] = row == EMPTY ? 0.f : ((dx ? fx : 1.f - fx) * (dy ? fy : 1.f - fy)) * (dz ? fz : 1.f - fz);
+    sum += w[v];
+  }
+  if (normalize && sum > 0.f) {
+#pragma unroll
+    for (int v = 0; v < 8; v++) w[v] = w[v] / sum;
+  }
+#pragma unroll
+  for (int v = 0; v < 8; v++) {
+    nb[i * 8 + v] = r[v];
+    wt[i * 8 + v] = w[v];
+  }
+}
+
+// y[i, c] = sum over v = 0..7 of x[nb[i, v], c] * wt[i, v], fused multiply-adds in v order (EMPTY reads 0): the
+// bake's weighted sum over the sample map (reference k_wsum, src/glb.cu:456-465).
+__global__ void __launch_bounds__(256) k_grid_sample_sum(const float* __restrict__ x, int C,
+                                                         const uint32_t* __restrict__ nb, const float* __restrict__ wt,
+                                                         i64 L, float* __restrict__ y) {
+  const i64 e = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= L * C) return;
+  const i64 i = e / C;
+  const int c = (int)(e - i * C);
+  float acc = 0.f;
+#pragma unroll
+  for (int v = 0; v < 8; v++) {
+    const uint32_t j = nb[i * 8 + v];
+    acc = fmaf(j != EMPTY ? x[(i64)j * C + c] : 0.f, wt[i * 8 + v], acc);
+  }
+  y[e] = acc;
+}
 }  // namespace
 
 void lookup(const SpConvCache& c, const Tensor& query, Tensor& rows) {
@@ -430,6 +494,31 @@ void lookup(const SpConvCache& c, const Tensor& query, Tensor& rows) {
                                                c.N ? (const ulonglong2*)c.htable.p : nullptr, c.hmask,
                                                c.hmaskd.defined() ? c.hmaskd.ptr<uint32_t>() : nullptr,
                                                c.N ? c.hbricks.ptr<uint32_t>() : nullptr, rows.ptr<int32_t>());
+  CK(hipGetLastError());
+}
+
+void grid_sample_map(const SpConvCache& c, const Tensor& grid, int batch, bool normalize, Tensor& nb, Tensor& wt) {
+  REQ(grid.dt == F32 && grid.dim() == 2 && grid.size(1) == 3, "grid must be f32 [L,3]");
+  const i64 L = grid.size(0);
+  REQ(nb.numel() == L * 8 && wt.dt == F32 && wt.numel() == L * 8, "nb must be u32 [L,8], wt f32 [L,8]");
+  if (L == 0) return;
+  REQ(c.N == 0 || c.htable.defined(), "the cache was built without keep_hash");
+  k_grid_sample_map<<<cdiv(L, 256), 256, 0, stream()>>>(
+      grid.ptr<float>(), L, batch, c.W, c.H, c.D, c.N ? (const ulonglong2*)c.htable.p : nullptr, c.hmask,
+      c.hmaskd.defined() ? c.hmaskd.ptr<uint32_t>() : nullptr, c.N ? c.hbricks.ptr<uint32_t>() : nullptr, normalize,
+      nb.ptr<uint32_t>(), wt.ptr<float>());
+  CK(hipGetLastError());
+}
+
+void grid_sample_sum(const Tensor& x, const Tensor& nb, const Tensor& wt, Tensor& y) {
+  REQ(x.dt == F32 && x.dim() == 2, "x must be f32 [M,C]");
+  const int C = (int)x.size(1);
+  const i64 L = nb.numel() / 8;
+  REQ(nb.numel() == L * 8 && wt.dt == F32 && wt.numel() == L * 8, "nb must be u32 [L,8], wt f32 [L,8]");
+  REQ(y.dt == F32 && y.numel() == L * C, "y must be f32 [L,C]");
+  if (L == 0 || C == 0) return;
+  k_grid_sample_sum<<<cdiv(L * C, 256), 256, 0, stream()>>>(x.ptr<float>(), C, nb.ptr<uint32_t>(), wt.ptr<float>(), L,
+                                                            y.ptr<float>());
   CK(hipGetLastError());
 }
 

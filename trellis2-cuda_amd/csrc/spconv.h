@@ -75,6 +75,16 @@ SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep
 // mesh.cu:14-19 (vhash_find) and spconv.cu:22-36, answered by the brick hash.
 void lookup(const SpConvCache& c, const Tensor& query, Tensor& rows);
 
+// Trilinear sample map of points grid f32 [L,3] (continuous voxel coordinates; voxel i's centre at i + 0.5) in batch
+// `batch` of a keep_hash cache: the 8 voxels around p - 0.5, corner v = dx*4 + dy*2 + dz, nb u32 [L,8] their rows
+// (EMPTY when absent or off-grid) and wt f32 [L,8] the trilinear weights (0 for EMPTY corners; with `normalize`
+// divided by the sum of the present ones). Reference: the bake's FlexGEMM neighbour map + weight builder on its
+// own voxel hash (src/glb.cu:547-550).
+void grid_sample_map(const SpConvCache& c, const Tensor& grid, int batch, bool normalize, Tensor& nb, Tensor& wt);
+// y[i] = sum_v x[nb[i,v]] * wt[i,v] in v order by fused multiply-adds (EMPTY reads 0); x f32 [M,C], y f32 [L,C]
+// (reference k_wsum, src/glb.cu:456-465,551-552).
+void grid_sample_sum(const Tensor& x, const Tensor& nb, const Tensor& wt, Tensor& y);
+
 // FlexiDualGrid quads from the kernel map, no hash probes (reference k_fdg_quads, src/mesh.cu:36-45): for voxel i
 // and axis a (e = 3i + a), if h[i,3+a] > 0 and the 4 voxels at the axis' edge offsets (all inside the 3x3x3
 // neighbourhood) exist, ok[e] = 1 and quad[e] = their rows, else ok[e] = 0 (quad[e] left untouched). h f32 [N,7],

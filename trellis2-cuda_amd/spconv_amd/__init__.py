@@ -29,7 +29,8 @@ SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build
            "spc_fdg_quads", "spc_cache_free", "spc_cache_info", "spc_cache_valid", "spc_conv_cfg",
            "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
            "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subm_conv_skip",
-           "spc_subdivide", "spc_subdivide_noalloc", "spc_subm_conv_replay")
+           "spc_subdivide", "spc_subdivide_noalloc", "spc_subm_conv_replay", "spc_grid_sample_map",
+           "spc_grid_sample_sum")
 
 _lib = None
 
@@ -67,6 +68,8 @@ def load_library():
     L.spc_subdivide.argtypes = [P, P, I64, P, P, ctypes.POINTER(I64)]
     L.spc_subdivide_noalloc.argtypes = [P, P, I64, P, P, P]
     L.spc_subm_conv_replay.argtypes = [P, P, P, P, I, I64, I, I, I, I, I, P, P]
+    L.spc_grid_sample_map.argtypes = [P, P, I64, I, I, P, P]
+    L.spc_grid_sample_sum.argtypes = [P, I64, I, P, P, I64, P]
     for name in SYMBOLS:
         if name != "spc_last_error":
             getattr(L, name).restype = I
@@ -203,6 +206,31 @@ def fdg_quads(cache: SpConvCache, h):
     ok = torch.empty(3 * cache.N, dtype=torch.int32, device=h.device)
     _check(load_library().spc_fdg_quads(cache._h, _ptr(h), _ptr(quad), _ptr(ok)))
     return quad, ok
+
+
+def grid_sample_map(cache: SpConvCache, grid, batch: int = 0, normalize: bool = False):
+    """Trilinear sample map of points grid (float32 [L,3], continuous voxel coordinates) on a keep_hash cache:
+    (nb int32 [L,8] rows or -1, wt float32 [L,8]); the bake's grid-sample map (src/glb.cu:547-550)."""
+    torch = _torch()
+    if grid.dtype != torch.float32 or grid.dim() != 2 or grid.shape[1] != 3:
+        raise ValueError("grid must be float32 [L,3]")
+    L = grid.shape[0]
+    nb = torch.empty((L, 8), dtype=torch.int32, device=grid.device)
+    wt = torch.empty((L, 8), dtype=torch.float32, device=grid.device)
+    _check(load_library().spc_grid_sample_map(cache._h, _ptr(grid), L, batch, 1 if normalize else 0, _ptr(nb),
+                                              _ptr(wt)))
+    return nb, wt
+
+
+def grid_sample_sum(x, nb, wt):
+    """y float32 [L,C] = sum_v x[nb[:,v]] * wt[:,v] (reference k_wsum, src/glb.cu:456-465)."""
+    torch = _torch()
+    if x.dtype != torch.float32 or x.dim() != 2:
+        raise ValueError("x must be float32 [M,C]")
+    L, C = nb.shape[0], x.shape[1]
+    y = torch.empty((L, C), dtype=torch.float32, device=x.device)
+    _check(load_library().spc_grid_sample_sum(_ptr(x), x.shape[0], C, _ptr(nb), _ptr(wt), L, _ptr(y)))
+    return y
 
 
 def spconv_cfg(N: int, Ci: int, Co: int):
