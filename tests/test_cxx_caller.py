@@ -1,0 +1,37 @@
+"""The C++ API as the reference's decoders call it (src/sdec.cu:15-18, 55, 92; src/spconv.h:6-16): a decoder-shaped
+translation unit (tests/cxx/decoder_caller.cpp) compiles against trellis2-cuda_amd/csrc/spconv.h and links against
+libspconv_amd.so (CPU test), and its conv / valid-list checks pass on the GPU (GPU test, the binary built by
+__graft_entry__.build())."""
+import os
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+PKG = os.path.join(ROOT, "trellis2-cuda_amd")
+
+
+def test_decoder_caller_compiles_and_links(tmp_path):
+    if not os.path.exists(os.path.join(PKG, "libspconv_amd.so")):
+        pytest.fail("libspconv_amd.so is not built")
+    out = tmp_path / "decoder_caller"
+    r = subprocess.run(["/opt/rocm/bin/hipcc", "-O1", "-std=c++17", "-I", os.path.join(PKG, "csrc"), "-o", str(out),
+                        os.path.join(HERE, "cxx", "decoder_caller.cpp"), "-L", PKG, "-lspconv_amd"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    syms = subprocess.run(["nm", "-DC", "--defined-only", os.path.join(PKG, "libspconv_amd.so")], capture_output=True,
+                          text=True).stdout
+    for s in ("build_neighbors(Tensor const&, int, int, int, bool)", "SpConvCache::valid(int)",
+              "spconv_cfg(int, int, int)", "subm_conv(Tensor const&, Tensor const&, Tensor const*, SpConvCache&)"):
+        assert s in syms, s
+
+
+@pytest.mark.gpu
+def test_decoder_caller_runs(gpu):
+    exe = os.path.join(HERE, "cxx", "decoder_caller")
+    assert os.path.exists(exe), "tests/cxx/decoder_caller is not built (run __graft_entry__.build())"
+    print("running tests/cxx/decoder_caller", flush=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr

@@ -18,6 +18,8 @@
 #include <string>
 #include <vector>
 
+#pragma GCC visibility push(default)  // exported for C++ callers (see spconv.h)
+
 [[noreturn]] void spc_fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 #define CK(x)                                                                                             \
   do {                                                                                                    \
@@ -80,3 +82,5 @@ std::vector<T> to_host_vec(const Tensor& t) {
 void dsync();
 
 __host__ __device__ inline int cdiv(i64 a, i64 b) { return (int)((a + b - 1) / b); }
+
+#pragma GCC visibility pop

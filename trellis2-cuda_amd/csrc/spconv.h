@@ -6,6 +6,10 @@
 
 #include "core.h"
 
+// The C++ API is exported from libspconv_amd.so (the library builds with hidden visibility otherwise), so C++
+// callers such as the sparse decoders link against it directly.
+#pragma GCC visibility push(default)
+
 // Neighbour cache for one coordinate set (reference src/spconv.h:5-11).
 //   nbr    [N,27] u32, 0xffffffff = no neighbour, offset v <-> (dx,dy,dz) = (v/9-1, v/3%3-1, v%3-1)
 //   gray   [N] i32   27-bit neighbour mask
@@ -175,3 +179,5 @@ i64 subdivide_noalloc_max_parents();
 void subdivide_noalloc_init();
 void subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, i64 n, int32_t* child_coords, int32_t* src,
                        i64* m_dev);
+
+#pragma GCC visibility pop
