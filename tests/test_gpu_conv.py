@@ -415,11 +415,12 @@ def test_halo_spill_gathered_and_skip(gpu):
     assert torch.equal(y3, y4), "skip variant != conv + add_skip on a cache with spill tiles"
 
 
-@pytest.mark.parametrize("nrows", [25309, 22000, 23800])
+@pytest.mark.parametrize("nrows", [25309, 22000, 23800, 10842, 3000, 700])
 def test_wide_tail_split(gpu, nrows, monkeypatch):
     """768 -> 768 (C2 coordinates, first nrows rows): 3 x ceil(nrows/128) tiles put 65-75 tiles on each XCD, more
     than its 64 concurrent workgroups, so the wide kernel splits each XCD's last tiles over several workgroups along
-    K and reduces their fp32 partials. Split and unsplit schedules differ only in the fp32 summation order: fp32
+    K and reduces their fp32 partials; at 10842 / 3000 / 700 rows (32, 9, 2-3 tiles per XCD) every tile is split,
+    over 2, 7 and 8 workgroups. Split and unsplit schedules differ only in the fp32 summation order: fp32
     outputs within rel-L2 1e-6, bf16 outputs within one bf16 ulp (+1e-5 absolute); every row of the split result
     is checked against the oracle. The coordinates are C2's spheres with a thicker shell (h = 2.35, 25 309 rows),
     so that the row-tile counts reach the split range."""

@@ -1837,6 +1837,25 @@ void launch_wide_dma(ConvArgs a) {
       a.part = ws.ptr<float>();
       a.grid = 8 * units;
     }
+  } else if (split_enabled() && slots > 0 && 2 * per <= slots) {
+    // too few tiles to fill half the slots (small N, e.g. C2's 85 x 3 tiles): every tile is split along its K
+    // stages over k = min(8, slots / c) workgroups, so each XCD runs about `slots` pieces at once
+    int units = 0, pslots = 0;
+    a.xs = 0;
+    for (int x = 0; x < 8; x++) {
+      a.xt0[x] = std::min(x * per, tiles);
+      const int c = std::min(per, tiles - a.xt0[x]);
+      a.xk[x] = c > 0 ? std::min(8, slots / c) : 1;
+      a.xpart0[x] = pslots;
+      if (a.xk[x] > 1) pslots += c * a.xk[x];
+      units = std::max(units, c * a.xk[x]);
+    }
+    a.xt0[8] = tiles;
+    if (pslots > 0) {
+      ws = empty({(i64)pslots * BM * 256}, F32);
+      a.part = ws.ptr<float>();
+      a.grid = 8 * units;
+    }
   }
   if (a.part) a.tsched = nullptr;  // the tail split keeps the XCD-contiguous walk
   k_conv_wide_dma<F16, BM><<<a.grid, 256, 0, stream()>>>(a);
