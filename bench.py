@@ -250,25 +250,33 @@ def measure(name, args, torch, np, sp, W, cpu, want_cpu, cpu_seconds, extras):
         # their parents' rows through the c2s map (no gathered child features are written)
         lgt = torch.from_numpy(lg.view(np.int16)).to(dev).view(torch.float16)
         xp = torch.randn((len(coords), ci), generator=g, device=dev).to(torch.bfloat16)
-        parts = {"subdivide": [], "kmap": [], "conv": [], "total": []}
-        for i in range(4):
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        parts = {"subdivide": [], "kmap": [], "conv": [], "total": [], "synced_total": []}
+        for i in range(6):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
             ev[0].record(stream)
-            ch, src = sp.subdivide(par, lgt)
+            ch, src, cc = sp.subdivide_build(par, lgt)
             ev[1].record(stream)
-            cc = sp.build_neighbors(ch.contiguous())
-            ev[2].record(stream)
             sp.subm_conv_gathered(xp, src, 3, w, b, cc, residual=res, act=act, out=y)
+            ev[2].record(stream)
+            # the same block with the reference's host read of the child count between subdivision and map
+            ch2, src2 = sp.subdivide(par, lgt)
             ev[3].record(stream)
+            cc2 = sp.build_neighbors(ch2.contiguous())
+            sp.subm_conv_gathered(xp, src2, 3, w, b, cc2, residual=res, act=act, out=y)
+            ev[4].record(stream)
             torch.cuda.synchronize()
             if i:
-                parts["subdivide"].append(ev[0].elapsed_time(ev[1]))
-                parts["kmap"].append(ev[1].elapsed_time(ev[2]))
-                parts["conv"].append(ev[2].elapsed_time(ev[3]))
-                parts["total"].append(ev[0].elapsed_time(ev[3]))
+                parts["subdivide"].append(ev[2].elapsed_time(ev[3]))
+                parts["kmap"].append(ev[0].elapsed_time(ev[1]))
+                parts["conv"].append(ev[1].elapsed_time(ev[2]))
+                parts["total"].append(ev[0].elapsed_time(ev[2]))
+                parts["synced_total"].append(ev[2].elapsed_time(ev[4]))
         e2e = {k + "_ms": round(float(np.median(v)), 4) for k, v in parts.items()}
-        e2e["note"] = ("subdivide -> build_neighbors -> subm_conv_gathered on a fresh cache each time (first-call "
-                       "schedules included), HIP events, median of 3")
+        e2e["note"] = ("total: subdivide_build (subdivision + children's map, no host sync between them) -> "
+                       "subm_conv_gathered on the fresh cache (first-call schedules included); kmap_ms is "
+                       "subdivide_build's part, conv_ms the conv's. synced_total: subdivide (host read of the count, "
+                       "as the reference) -> build_neighbors -> the same conv; subdivide_ms that path's "
+                       "subdivision. HIP events, median of 5")
         # the reference block's second half on the same children (src/sdec.cu:76-84): conv1's output h1 [n, 8*Co]
         # (random here) -> child rows -> LayerNorm -> SiLU -> conv2 (Co -> Co) -> skip add from the parents' x
         co2 = co

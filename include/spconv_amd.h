@@ -174,6 +174,15 @@ int spc_subm_conv_replay(const void* x, const void* w, const void* b, const void
 int spc_subdivide(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
                   int32_t* src, int64_t* m);
 
+/* Subdivision and the children's kernel map in one call, with no host sync between them: children into
+ * child_coords int32 [>= 8n, 4] and src int32 [>= 8n] as spc_subdivide, *m (host) their count, *out a cache equal
+ * to spc_build_neighbors(child_coords, *m, W, H, D). The map build is launched for the 8n capacity and stops at the
+ * count on the device; the count is copied back while the build runs.
+ * Replaces: SDecoder::c2s -- k_c2s_count / scan / host read of the count / k_c2s_emit, then build_neighbors on the
+ * children (src/sdec.cu:45-56). */
+int spc_subdivide_build(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int W, int H, int D,
+                        int32_t* child_coords, int32_t* src, int64_t* m, spc_cache** out);
+
 /* spc_subdivide without allocating and without waiting: the same children into child_coords int32 [>= 8n, 4] and
  * src int32 [>= 8n], their count into *m_dev (DEVICE int64). No counterpart in the reference: it is for callers that
  * cannot allocate device memory or block on the host (code under HIP graph capture, tight serving loops). Its

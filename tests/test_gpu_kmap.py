@@ -274,3 +274,41 @@ def test_grid_sample(gpu, name):
     # another batch index finds nothing
     nb3, wt3 = sp.grid_sample_map(cache, tp, batch=1)
     assert bool((nb3 == -1).all()) and bool((wt3 == 0).all())
+
+
+@pytest.mark.parametrize("name", ["c1", "c5"])
+def test_subdivide_build(gpu, name):
+    """subdivide_build (no host sync between the subdivision and the map build: launches sized for the 8n-child
+    capacity, kernels stopped at the device-side count) equals subdivide followed by build_neighbors: children, src,
+    nbr, gray, sorted and the valid lists bit for bit, the children's map against the oracle, and a conv on either
+    cache gives identical outputs."""
+    par = coords(name)
+    cfg = W.CONFIGS["c5"]
+    lg = W.keep_logits(len(par), cfg.keep_frac, cfg.seed)
+    tc = torch.from_numpy(par).to(gpu)
+    tl = torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16)
+    print(f"subdivide_build case {name} parents={len(par)}", flush=True)
+    cc, src, cache = sp.subdivide_build(tc, tl)
+    rc, rs = sp.subdivide(tc, tl)
+    assert torch.equal(cc, rc) and torch.equal(src, rs)
+    ref = sp.build_neighbors(rc.contiguous())
+    a, b = cache.tensors(), ref.tensors()
+    for x, y in zip(a, b):
+        assert x.shape == y.shape and torch.equal(x, y)
+    for B1 in (32, 128):
+        for x, y in zip(cache.valid(B1), ref.valid(B1)):
+            assert torch.equal(x, y)
+    if name == "c1":
+        onbr, ogray, _, osrt = oracle.build_neighbors(rc.cpu().numpy())
+        np.testing.assert_array_equal(a[0].cpu().numpy().view(np.uint32), onbr)
+        np.testing.assert_array_equal(a[2].cpu().numpy(), osrt)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(3)
+    x = torch.randn((len(cc), 64), generator=g, device=gpu).to(torch.bfloat16)
+    w = (torch.randn((64, 27, 64), generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    y1 = sp.subm_conv_fused(x, w, None, cache, act=sp.ACT_SILU, out_dtype=torch.float32)
+    y2 = sp.subm_conv_fused(x, w, None, ref, act=sp.ACT_SILU, out_dtype=torch.float32)
+    assert torch.equal(y1, y2)
+    # no parents: empty level
+    e_cc, e_src, e_cache = sp.subdivide_build(tc[:0], tl[:0])
+    assert e_cc.shape == (0, 4) and e_src.shape == (0,) and e_cache.N == 0

@@ -275,6 +275,20 @@ SPC_API int spc_grid_sample_sum(const float* x, int64_t M, int C, const uint32_t
   });
 }
 
+SPC_API int spc_subdivide_build(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int W, int H, int D,
+                                int32_t* child_coords, int32_t* src, int64_t* m, spc_cache** out) {
+  return guarded([&] {
+    REQ(m && out, "m or out is null");
+    REQ(n >= 0 && (n == 0 || (coords && logits_f16 && child_coords && src)), "null argument");
+    auto h = std::make_unique<spc_cache>();
+    UpsampleLevel lv = subdivide_build(borrow(coords, {n, 4}, I32), borrow(logits_f16, {n, 8}, F16), W, H, D,
+                                       child_coords, src);
+    h->c = std::move(lv.cache);
+    *m = lv.coords.size(0);
+    *out = h.release();
+  });
+}
+
 SPC_API int spc_subdivide(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
                           int32_t* src, int64_t* m) {
   return guarded([&] {

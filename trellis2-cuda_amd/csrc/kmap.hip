@@ -62,7 +62,9 @@ __device__ __forceinline__ uint32_t brick_find(const ulonglong2* __restrict__ t,
 // counts, then one block sums them and stores the mask of the smallest power-of-two table with at least twice
 // that many slots (load <= 0.5), capped at the allocated capacity.
 __global__ void __launch_bounds__(256) k_brick_runs(const int4* __restrict__ c, i64 n, int W4, int H4, int D4,
-                                                    uint32_t* __restrict__ part) {
+                                                    uint32_t* __restrict__ part, const uint32_t* __restrict__ ndev) {
+  if (ndev) n = min<i64>(n, *ndev);  // device-side row count (rows past it are capacity)
+  if ((i64)blockIdx.x * blockDim.x >= n) return;  // k_brick_mask reads only the blocks below n
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
   int head = 0;
   if (i < n) {
@@ -79,8 +81,9 @@ __global__ void __launch_bounds__(256) k_brick_runs(const int4* __restrict__ c, 
   if (threadIdx.x == 0) part[blockIdx.x] = (uint32_t)cnt;
 }
 __global__ void __launch_bounds__(1024) k_brick_mask(const uint32_t* __restrict__ part, i64 nb, uint64_t capmax,
-                                                     uint32_t* __restrict__ maskp) {
+                                                     uint32_t* __restrict__ maskp, const uint32_t* __restrict__ ndev) {
   __shared__ uint64_t red[16];
+  if (ndev) nb = min<i64>(nb, ((i64)*ndev + 255) / 256);  // the blocks k_brick_runs wrote
   uint64_t sum = 0;
   for (i64 b = threadIdx.x; b < nb; b += 1024) sum += part[b];
 #pragma unroll
@@ -100,7 +103,8 @@ __global__ void __launch_bounds__(1024) k_brick_mask(const uint32_t* __restrict_
 // shared counter), and the brick's 64-entry record is cleared by that voxel's wavefront.
 __global__ void __launch_bounds__(256) k_brick_insert(const int4* __restrict__ c, i64 n, int W4, int H4, int D4,
                                                       ulonglong2* __restrict__ t, uint32_t mask0, const uint32_t* __restrict__ maskp,
-                                                      uint4* __restrict__ bricks) {
+                                                      uint4* __restrict__ bricks, const uint32_t* __restrict__ ndev) {
+  if (ndev) n = min<i64>(n, *ndev);
   const uint32_t mask = maskp ? *maskp : mask0;
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
   uint64_t k = HEMPTY;
@@ -146,7 +150,8 @@ __global__ void __launch_bounds__(256) k_brick_insert(const int4* __restrict__ c
 
 __global__ void __launch_bounds__(256) k_brick_fill(const int4* __restrict__ c, i64 n, int W4, int H4, int D4,
                                                     const ulonglong2* __restrict__ t, uint32_t mask0, const uint32_t* __restrict__ maskp,
-                                                    uint32_t* __restrict__ bricks) {
+                                                    uint32_t* __restrict__ bricks, const uint32_t* __restrict__ ndev) {
+  if (ndev) n = min<i64>(n, *ndev);
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const uint32_t mask = maskp ? *maskp : mask0;
@@ -168,10 +173,12 @@ __global__ void __launch_bounds__(NVV) k_neighbors_vox(const int4* __restrict__ 
                                                        uint32_t mask0, const uint32_t* __restrict__ maskp,
                                                        const uint32_t* __restrict__ bricks,
                                                        uint32_t* __restrict__ nbr, int32_t* __restrict__ gray,
-                                                       uint32_t* __restrict__ bin) {
+                                                       uint32_t* __restrict__ bin, const uint32_t* __restrict__ ndev) {
   __shared__ uint32_t rows[NVV * 27];
+  if (ndev) n = min<i64>(n, *ndev);
   const uint32_t mask = maskp ? *maskp : mask0;
   const i64 v0 = (i64)blockIdx.x * NVV;
+  if (v0 >= n) return;  // a capacity block past the device-side count (uniform over the workgroup)
   const int nv = (int)min<i64>(NVV, n - v0);
   const int tid = threadIdx.x;
   const bool live = tid < nv;
@@ -322,10 +329,13 @@ __global__ void k_c2s_emit(const uint4* __restrict__ lg, const int4* __restrict_
 }
 }  // namespace
 
-SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep_hash) {
-  REQ(coords.dt == I32 && coords.dim() == 2 && coords.size(1) == 4, "coords must be int32 [N,4]");
+namespace {
+// The build over rows [0, n) of coords; with ndev (device u32) the row count is read on the device and n is only a
+// capacity bound: every launch is sized for n and its kernels stop at *ndev, so nothing here waits for the host.
+// The cache's tensors then have n rows, of which the first *ndev are meaningful.
+SpConvCache build_neighbors_impl(const int4* coords, i64 n, const uint32_t* ndev, int W, int H, int D,
+                                 bool keep_hash) {
   REQ(W > 0 && H > 0 && D > 0, "grid %dx%dx%d", W, H, D);
-  i64 n = coords.size(0);
   REQ(n < (1ll << 31) - 1, "too many voxels %lld", (long long)n);
   SpConvCache c;
   c.N = (int)n;
@@ -350,22 +360,20 @@ SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep
     Tensor part = empty({nb}, I32);
     maskt = empty({1}, I32);
     maskp = maskt.ptr<uint32_t>();
-    k_brick_runs<<<nb, 256, 0, s>>>(coords.ptr<int4>(), n, W4, H4, D4, part.ptr<uint32_t>());
-    k_brick_mask<<<1, 1024, 0, s>>>(part.ptr<uint32_t>(), nb, cap, maskp);
+    k_brick_runs<<<nb, 256, 0, s>>>(coords, n, W4, H4, D4, part.ptr<uint32_t>(), ndev);
+    k_brick_mask<<<1, 1024, 0, s>>>(part.ptr<uint32_t>(), nb, cap, maskp, ndev);
   }
   k_table_clear<<<(int)std::min<i64>(cdiv((i64)cap, 256), 4096), 256, 0, s>>>(t, mask0, maskp);
   // at most n occupied bricks: the table (capacity >= 2n) never fills. Brick records are indexed by the row of
   // the voxel that inserted the brick, so the record array has n slots (only occupied bricks' records are touched).
   Tensor bricks = empty({n * 64}, I32);
-  k_brick_insert<<<cdiv(n, 256), 256, 0, s>>>(coords.ptr<int4>(), n, W4, H4, D4, t, mask0, maskp,
-                                              (uint4*)bricks.p);
-  k_brick_fill<<<cdiv(n, 256), 256, 0, s>>>(coords.ptr<int4>(), n, W4, H4, D4, t, mask0, maskp,
-                                            bricks.ptr<uint32_t>());
-  k_neighbors_vox<<<cdiv(n, NVV), NVV, 0, s>>>(coords.ptr<int4>(), n, W, H, D, t, mask0, maskp,
-                                               bricks.ptr<uint32_t>(), c.nbr.ptr<uint32_t>(),
-                                               c.gray.ptr<int32_t>(), bin.ptr<uint32_t>());
+  k_brick_insert<<<cdiv(n, 256), 256, 0, s>>>(coords, n, W4, H4, D4, t, mask0, maskp, (uint4*)bricks.p, ndev);
+  k_brick_fill<<<cdiv(n, 256), 256, 0, s>>>(coords, n, W4, H4, D4, t, mask0, maskp, bricks.ptr<uint32_t>(), ndev);
+  k_neighbors_vox<<<cdiv(n, NVV), NVV, 0, s>>>(coords, n, W, H, D, t, mask0, maskp, bricks.ptr<uint32_t>(),
+                                               c.nbr.ptr<uint32_t>(), c.gray.ptr<int32_t>(), bin.ptr<uint32_t>(),
+                                               ndev);
   CK(hipGetLastError());
-  stable_argsort27(bin.ptr<uint32_t>(), n, c.sorted.ptr<int32_t>());
+  stable_argsort27(bin.ptr<uint32_t>(), n, c.sorted.ptr<int32_t>(), ndev);
   c.W = W;
   c.H = H;
   c.D = D;
@@ -376,6 +384,12 @@ SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep
     c.hmaskd = maskt;
   }
   return c;
+}
+}  // namespace
+
+SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep_hash) {
+  REQ(coords.dt == I32 && coords.dim() == 2 && coords.size(1) == 4, "coords must be int32 [N,4]");
+  return build_neighbors_impl(coords.ptr<int4>(), coords.size(0), nullptr, W, H, D, keep_hash);
 }
 
 namespace {
@@ -649,24 +663,36 @@ __global__ void __launch_bounds__(1024) k_tile_lpt(const uint32_t* __restrict__ 
     }
   }
   __syncthreads();
-  // stable placement: each bucket is filled in tile order by one pass per chunk of 1024 tiles, ranking a tile
-  // among the chunk's tiles of its bucket with a block-wide count of the lower-numbered ones
-  __shared__ uint32_t key[1024];
+  // stable placement, one pass per chunk of 1024 tiles: a tile's rank among the chunk's tiles of its bucket is the
+  // count of lower lanes of its wavefront holding the same bucket (5 ballots) plus the wavefronts before it
+  __shared__ uint32_t wcnt[16][32];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint64_t lt = (1ull << lane) - 1ull;
   for (int base = 0; base < nt; base += 1024) {
+    for (int e = threadIdx.x; e < 16 * 32; e += blockDim.x) wcnt[e >> 5][e & 31] = 0;
+    __syncthreads();
     const int t = base + (int)threadIdx.x;
     const uint32_t k = t < nt ? 27 - min(cost[t], 27u) : 31u;
-    key[threadIdx.x] = k;
-    __syncthreads();
-    uint32_t rank = 0;
-    for (int u = 0; u < (int)threadIdx.x; u++) rank += key[u] == k;
-    if (t < nt) order[start[k] + rank] = t;
-    __syncthreads();
-    // advance the bucket starts by this chunk's counts
-    if (threadIdx.x < 32) {
-      uint32_t c = 0;
-      for (int u = 0; u < 1024; u++) c += key[u] == threadIdx.x;
-      start[threadIdx.x] += c;
+    uint64_t peers = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 5; b++) {
+      const uint64_t m = __ballot((k >> b) & 1u);
+      peers &= ((k >> b) & 1u) ? m : ~m;
     }
+    const uint32_t rank = (uint32_t)__popcll(peers & lt);
+    if (rank == 0) wcnt[wv][k] = (uint32_t)__popcll(peers);
+    __syncthreads();
+    if (threadIdx.x < 32) {  // bucket b: exclusive offsets of the wavefronts, then advance the bucket start
+      uint32_t run = start[threadIdx.x];
+      for (int w = 0; w < 16; w++) {
+        const uint32_t c = wcnt[w][threadIdx.x];
+        wcnt[w][threadIdx.x] = run;
+        run += c;
+      }
+      start[threadIdx.x] = run;
+    }
+    __syncthreads();
+    if (t < nt) order[wcnt[wv][k] + rank] = t;
     __syncthreads();
   }
 }
@@ -753,6 +779,70 @@ Subdivision subdivide(const Tensor& coords, const Tensor& logits) {
                                             o.coords.ptr<int4>(), o.src.ptr<int32_t>());
     CK(hipGetLastError());
   }
+  return o;
+}
+
+// ------------------------------------------------------------------------------------------ subdivision + map, no sync
+namespace {
+// One pinned host word and an event per device: the child count is copied back while the map build runs.
+struct CountReadback {
+  uint32_t* host = nullptr;
+  hipEvent_t ev = nullptr;
+};
+CountReadback& count_readback() {
+  static CountReadback rb[64];
+  int dev = 0;
+  CK(hipGetDevice(&dev));
+  REQ(dev >= 0 && dev < 64, "device %d", dev);
+  CountReadback& r = rb[dev];
+  if (!r.host) {
+    CK(hipHostMalloc((void**)&r.host, sizeof(uint32_t), hipHostMallocDefault));
+    CK(hipEventCreateWithFlags(&r.ev, hipEventDisableTiming));
+  }
+  return r;
+}
+}  // namespace
+
+UpsampleLevel subdivide_build(const Tensor& coords, const Tensor& logits, int W, int H, int D, int32_t* coords_out,
+                              int32_t* src_out) {
+  REQ(coords.dt == I32 && coords.dim() == 2 && coords.size(1) == 4, "coords must be int32 [N,4]");
+  const i64 n = coords.size(0);
+  REQ(logits.dt == F16 && logits.numel() == n * 8, "logits must be fp16 [N,8]");
+  REQ(8 * n < (1ll << 31) - 1, "too many parents %lld", (long long)n);
+  UpsampleLevel o;
+  if (n == 0) {
+    o.coords = empty({0, 4}, I32);
+    o.src = empty({0}, I32);
+    o.cache = build_neighbors(o.coords, W, H, D);
+    return o;
+  }
+  hipStream_t s = stream();
+  const i64 cap = 8 * n;  // children at most
+  Tensor cc = coords_out ? borrow(coords_out, {cap, 4}, I32) : empty({cap, 4}, I32);
+  Tensor src = src_out ? borrow(src_out, {cap}, I32) : empty({cap}, I32);
+  Tensor off = empty({n + 1}, I32);
+  k_c2s_count<<<cdiv(n + 1, 256), 256, 0, s>>>(logits.ptr<uint4>(), n, off.ptr<uint32_t>());
+  excl_scan_u32(off.ptr<uint32_t>(), off.ptr<uint32_t>(), n + 1, nullptr);
+  const uint32_t* mdev = off.ptr<uint32_t>() + n;  // the child count, on the device
+  CountReadback& rb = count_readback();
+  CK(hipMemcpyAsync(rb.host, mdev, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  CK(hipEventRecord(rb.ev, s));
+  k_c2s_emit<<<cdiv(n, 256), 256, 0, s>>>(logits.ptr<uint4>(), coords.ptr<int4>(), off.ptr<uint32_t>(), n,
+                                          cc.ptr<int4>(), src.ptr<int32_t>());
+  CK(hipGetLastError());
+  // the children's map, sized for the capacity and stopped at the device-side count by every kernel
+  SpConvCache c = build_neighbors_impl(cc.ptr<int4>(), cap, mdev, W, H, D, false);
+  // every kernel of the build is queued: waiting for the count now leaves the GPU busy
+  CK(hipEventSynchronize(rb.ev));
+  const i64 m = *rb.host;
+  REQ(m <= cap, "child count %lld above %lld", (long long)m, (long long)cap);
+  c.N = (int)m;
+  c.nbr = c.nbr.slice0(0, m);
+  c.gray = c.gray.slice0(0, m);
+  c.sorted = c.sorted.slice0(0, m);
+  o.coords = cc.slice0(0, m);
+  o.src = src.slice0(0, m);
+  o.cache = std::move(c);
   return o;
 }
 

@@ -54,8 +54,12 @@ __device__ __forceinline__ void rank_chunks(const uint32_t* __restrict__ kin, co
 template <int RCH>
 __global__ void __launch_bounds__(RT) k_rs_count(const uint32_t* __restrict__ keys, i64 n, int shift,
                                                  uint32_t* __restrict__ hist, int ntiles, uint32_t* __restrict__ zero,
-                                                 int zn) {
+                                                 int zn, const uint32_t* __restrict__ ndev) {
   __shared__ uint32_t cnt[NBUK];
+  if (ndev) {  // device-side key count: tiles past it are skipped (the digit scan reads only the tiles below it)
+    n = min<i64>(n, *ndev);
+    if (blockIdx.x > 0 && (i64)blockIdx.x * (RT * RCH) >= n) return;
+  }
   if (zero && blockIdx.x == 0)
     for (int i = threadIdx.x; i < zn; i += RT) zero[i] = 0;
   for (int d = threadIdx.x; d < NBUK; d += RT) cnt[d] = 0;
@@ -73,8 +77,13 @@ __global__ void __launch_bounds__(RT) k_rs_count(const uint32_t* __restrict__ ke
 template <int RCH>
 __global__ void __launch_bounds__(RT) k_rs_scatter(const uint32_t* __restrict__ kin, const int32_t* __restrict__ vin,
                                                    uint32_t* __restrict__ kout, int32_t* __restrict__ vout, i64 n,
-                                                   int shift, const uint32_t* __restrict__ start, int ntiles) {
+                                                   int shift, const uint32_t* __restrict__ start, int ntiles,
+                                                   const uint32_t* __restrict__ ndev) {
   __shared__ uint32_t cnt[RT / 64][NBUK];
+  if (ndev) {
+    n = min<i64>(n, *ndev);
+    if (blockIdx.x > 0 && (i64)blockIdx.x * (RT * RCH) >= n) return;  // no keys in this tile
+  }
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   for (int d = threadIdx.x; d < NBUK; d += RT)
     for (int w = 0; w < RT / 64; w++) cnt[w][d] = 0;
@@ -115,11 +124,14 @@ __global__ void __launch_bounds__(RT) k_rs_scatter(const uint32_t* __restrict__ 
 // scanned to exclusive tile starts in `start` (not in place: the counts stay intact for such a fallback read).
 __global__ void __launch_bounds__(RT) k_rs_digit_scan(const uint32_t* __restrict__ cnt,
                                                       uint32_t* __restrict__ start, uint64_t* __restrict__ dsum,
-                                                      int ntiles, uint32_t spin_limit) {
+                                                      int ntiles, uint32_t spin_limit, const uint32_t* __restrict__ ndev,
+                                                      int tile_keys) {
   __shared__ uint32_t red[RT / 64];
   const int d = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t* row = cnt + (i64)d * ntiles;
-  uint32_t* orow = start + (i64)d * ntiles;
+  const int stride = ntiles;  // rows keep the capacity stride
+  const uint32_t* row = cnt + (i64)d * stride;
+  uint32_t* orow = start + (i64)d * stride;
+  if (ndev) ntiles = max(1, min(ntiles, (int)(((i64)*ndev + tile_keys - 1) / tile_keys)));  // tiles with keys
   auto wg_sum = [&](uint32_t v) __attribute__((always_inline)) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
@@ -144,7 +156,7 @@ __global__ void __launch_bounds__(RT) k_rs_digit_scan(const uint32_t* __restrict
       // not published within the limit: sum digit e's row of tile counts here (they are complete: the count
       // kernel ran before this launch), so the start is exact whatever the workgroup schedule
       uint32_t s = 0;
-      for (int i = 0; i < ntiles; i++) s += cnt[(i64)e * ntiles + i];
+      for (int i = 0; i < ntiles; i++) s += cnt[(i64)e * stride + i];
       w = s;
     }
     below += (uint32_t)w;
@@ -175,7 +187,8 @@ __global__ void __launch_bounds__(RT) k_rs_digit_scan(const uint32_t* __restrict
 }
 }  // namespace
 
-void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bits, int32_t* vals_out) {
+void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bits, int32_t* vals_out,
+                       const uint32_t* ndev) {
   if (n <= 0) return;
   REQ(n < (1ll << 31), "sort size %lld", (long long)n);
   REQ(bits >= 1 && bits <= 32, "key bits %d", bits);
@@ -208,17 +221,19 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
     const int shift = p * RBITS;
     uint32_t* z = p == 0 ? (uint32_t*)dsum : nullptr;  // the first count kernel zeroes every pass's digit sums
     const int zn = (int)swords;
-    if (rch == 16) k_rs_count<16><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
-    else if (rch == 8) k_rs_count<8><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
-    else k_rs_count<4><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn);
-    k_rs_digit_scan<<<NBUK, RT, 0, s>>>(h, st, dsum + p * NBUK, ntiles, spin_limit);
-    if (rch == 16) k_rs_scatter<16><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles);
-    else if (rch == 8) k_rs_scatter<8><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles);
-    else k_rs_scatter<4><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles);
+    if (rch == 16) k_rs_count<16><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
+    else if (rch == 8) k_rs_count<8><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
+    else k_rs_count<4><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
+    k_rs_digit_scan<<<NBUK, RT, 0, s>>>(h, st, dsum + p * NBUK, ntiles, spin_limit, ndev, RT * rch);
+    if (rch == 16) k_rs_scatter<16><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles, ndev);
+    else if (rch == 8) k_rs_scatter<8><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles, ndev);
+    else k_rs_scatter<4><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles, ndev);
     kin = kout;
     vin = vout;
   }
   CK(hipGetLastError());
 }
 
-void stable_argsort27(const uint32_t* keys, i64 n, int32_t* order) { stable_sort_pairs(keys, nullptr, n, 27, order); }
+void stable_argsort27(const uint32_t* keys, i64 n, int32_t* order, const uint32_t* ndev) {
+  stable_sort_pairs(keys, nullptr, n, 27, order, ndev);
+}

@@ -172,6 +172,17 @@ struct Subdivision {
   Tensor coords, src;  // int32 [M,4], int32 [M]
 };
 Subdivision subdivide(const Tensor& coords, const Tensor& logits_f16);
+// Subdivision and the children's kernel map with no host sync in between (the reference waits for the child count
+// at src/sdec.cu:52 before it can size the map): every launch is sized for the 8n-child capacity and its kernels stop
+// at the count on the device; the count is copied back while the map build runs and read once all of it is queued.
+// coords_out / src_out: optional caller buffers of >= 8n rows (else allocated). The cache equals
+// build_neighbors(coords, W, H, D) on the children.
+struct UpsampleLevel {
+  Tensor coords, src;  // int32 [M,4], int32 [M] (views of the capacity buffers)
+  SpConvCache cache;
+};
+UpsampleLevel subdivide_build(const Tensor& coords, const Tensor& logits_f16, int W, int H, int D,
+                              int32_t* coords_out = nullptr, int32_t* src_out = nullptr);
 // The same children written into caller buffers of >= 8n rows, the count into device memory (*m_dev, int64), with no
 // allocation and no host sync: its scratch is a static device array (see kmap.hip), so n <= the maximum below and
 // concurrent calls on one GPU race. init() looks up the array's device address on the current device.

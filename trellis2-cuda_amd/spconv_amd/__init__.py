@@ -30,7 +30,7 @@ SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build
            "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
            "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subm_conv_skip",
            "spc_subdivide", "spc_subdivide_noalloc", "spc_subm_conv_replay", "spc_grid_sample_map",
-           "spc_grid_sample_sum")
+           "spc_grid_sample_sum", "spc_subdivide_build")
 
 _lib = None
 
@@ -70,6 +70,7 @@ def load_library():
     L.spc_subm_conv_replay.argtypes = [P, P, P, P, I, I64, I, I, I, I, I, P, P]
     L.spc_grid_sample_map.argtypes = [P, P, I64, I, I, P, P]
     L.spc_grid_sample_sum.argtypes = [P, I64, I, P, P, I64, P]
+    L.spc_subdivide_build.argtypes = [P, P, I64, I, I, I, P, P, ctypes.POINTER(I64), PP]
     for name in SYMBOLS:
         if name != "spc_last_error":
             getattr(L, name).restype = I
@@ -389,6 +390,20 @@ def subdivide(coords, logits_f16):
     m = ctypes.c_int64()
     _check(load_library().spc_subdivide(_ptr(coords), _ptr(logits_f16), n, _ptr(cc), _ptr(src), ctypes.byref(m)))
     return cc[:m.value], src[:m.value]
+
+
+def subdivide_build(coords, logits_f16, W: int = 4096, H: int = 4096, D: int = 4096):
+    """(child coords int32 [M,4], src int32 [M], SpConvCache of the children) with no host sync between the
+    subdivision and the map build (reference SDecoder::c2s, src/sdec.cu:45-56)."""
+    torch = _torch()
+    n = coords.shape[0]
+    cc = torch.empty((max(8 * n, 1), 4), dtype=torch.int32, device=coords.device)
+    src = torch.empty((max(8 * n, 1),), dtype=torch.int32, device=coords.device)
+    m = ctypes.c_int64()
+    h = ctypes.c_void_p()
+    _check(load_library().spc_subdivide_build(_ptr(coords), _ptr(logits_f16), n, W, H, D, _ptr(cc), _ptr(src),
+                                              ctypes.byref(m), ctypes.byref(h)))
+    return cc[:m.value], src[:m.value], SpConvCache(h, m.value, coords.device)
 
 
 def source_digest() -> str:
