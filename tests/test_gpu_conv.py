@@ -160,6 +160,18 @@ def test_configs_all_rows(gpu, name):
     run_case(gpu, c, cfg.ci, cfg.co, act=act, res_dt=res, seed=cfg.seed)
 
 
+def test_halo128_children(gpu, monkeypatch):
+    """The halo kernel at Ci = 128 (opt-in, SPCONV_HALO128): two K chunks per offset, 128-row windows, spill tiles
+    to the gathering kernel; c5-style children, every row against the oracle, plain and gathered."""
+    monkeypatch.setenv("SPCONV_HALO128", "1")
+    par = W.shell_coords(W.CONFIGS["c1"])
+    lg = W.keep_logits(len(par), 0.5, 9)
+    gc, _ = sp.subdivide(torch.from_numpy(par).to(gpu), torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16))
+    c = gc.cpu().numpy()
+    run_case(gpu, c, 128, 64, act=1, res_dt="bf16", seed=5)
+    run_case(gpu, c, 128, 64, in_dt="f16", out_dt="f32", seed=6)
+
+
 def test_c5_children(gpu):
     """C5's children (the subdivided 1024^3 level, 128 -> 64, bias + SiLU), every output row checked."""
     cfg = W.CONFIGS["c5"]

@@ -1017,62 +1017,82 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
     for (int t = 0; t < T; t++) acc[i][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.w_bytes);
   const uint16_t* idx16 = (const uint16_t*)idxL;
-  auto wload = [&](int v, u32x4 (&w)[T][S]) __attribute__((always_inline)) {
+  // The K loop walks stages (offset v, K chunk kc): KS 32-channel MFMA steps per stage, NKC chunks per offset (one
+  // at Ci <= 64; two at Ci = 128, so a stage's operands stay within the register budget).
+  constexpr int KS = S < 2 ? S : 2, NKC = S / KS;
+  static_assert(NKC * KS == S, "K chunks");
+  auto wload = [&](int v, int kc, u32x4 (&w)[T][KS]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < T; t++)
 #pragma unroll
-      for (int m = 0; m < S; m++)
-        w[t][m] = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(((v * 4 + wc * T + t) * S + m) * 64 + lane) * 16u,
-                                                        0, 0);
+      for (int m = 0; m < KS; m++)
+        w[t][m] = __builtin_amdgcn_raw_buffer_load_b128(
+            rw, (uint32_t)(((v * 4 + wc * T + t) * S + kc * KS + m) * 64 + lane) * 16u, 0, 0);
   };
-  // A operands of offset v for every group (idle groups read the zero row: LDS reads are cheap, and reading them
-  // unconditionally lets the reads of the next offset be issued before this offset's MFMAs). Lane quarter q4 takes
-  // channels (q4*S + m)*8 .. +8 in step m, the weight repack's order.
-  auto aload = [&](int v, u32x4 (&av)[G][S]) __attribute__((always_inline)) {
+  // A operands of stage (v, kc) for every group (idle groups read the zero row: LDS reads are cheap, and reading
+  // them unconditionally lets the reads of the next stage be issued before this stage's MFMAs). Lane quarter q4
+  // takes channels (q4*S + m)*8 .. +8 in step m, the weight repack's order.
+  auto aload = [&](int v, int kc, u32x4 (&av)[G][KS]) __attribute__((always_inline)) {
     int u[G];
 #pragma unroll
     for (int i = 0; i < G; i++) u[i] = idx16[v * B + wr * 16 * G + i * 16 + r16];
 #pragma unroll
     for (int i = 0; i < G; i++)
 #pragma unroll
-      for (int m = 0; m < S; m++) av[i][m] = halo[u[i] * RU + ((q4 * S + m) ^ (u[i] & (RU - 1)))];
+      for (int m = 0; m < KS; m++) av[i][m] = halo[u[i] * RU + ((q4 * S + kc * KS + m) ^ (u[i] & (RU - 1)))];
   };
-  auto compute = [&](int v, const u32x4 (&w)[T][S], const u32x4 (&av)[G][S]) __attribute__((always_inline)) {
+  auto compute = [&](int v, const u32x4 (&w)[T][KS], const u32x4 (&av)[G][KS]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < G; i++) {
       if ((gms[i] >> v) & 1u) {
 #pragma unroll
-        for (int m = 0; m < S; m++)
+        for (int m = 0; m < KS; m++)
 #pragma unroll
           for (int t = 0; t < T; t++) acc[i][t] = mfma16<F16>(av[i][m], w[t][m], acc[i][t]);
       }
     }
   };
-  // offsets of this wavefront in ascending order; the weights (from L2) and A operands (from LDS) of the next one
-  // are requested while this one computes. The weight load is unconditional -- the last offset reloads itself --
-  // so the compiler's wait counts stay exact.
+  // stages of this wavefront's offsets in ascending order; the weights (from L2) and A operands (from LDS) of the
+  // next stage are requested while this one computes. The loads are unconditional -- the last stage reloads
+  // itself -- so the compiler's wait counts stay exact.
   if (wmask) {
     uint32_t m = wmask;
-    int v = __builtin_ctz(m);
+    int v = __builtin_ctz(m), kc = 0;
     m &= m - 1;
-    u32x4 wa[T][S], wb[T][S], aa[G][S], ab[G][S];
-    wload(v, wa);
-    aload(v, aa);
+    bool more = true;
+    auto advance = [&](int& nv, int& nk) __attribute__((always_inline)) {
+      if (kc + 1 < NKC) {
+        nv = v;
+        nk = kc + 1;
+      } else if (m) {
+        nv = __builtin_ctz(m);
+        nk = 0;
+        m &= m - 1;
+      } else {
+        nv = v;
+        nk = kc;
+        more = false;
+      }
+    };
+    u32x4 wa[T][KS], wb[T][KS], aa[G][KS], ab[G][KS];
+    wload(v, kc, wa);
+    aload(v, kc, aa);
     for (;;) {
-      int vn = m ? __builtin_ctz(m) : v;
-      wload(vn, wb);
-      aload(vn, ab);
+      int vn, kn;
+      advance(vn, kn);
+      wload(vn, kn, wb);
+      aload(vn, kn, ab);
       compute(v, wa, aa);
-      if (!m) break;
-      m &= m - 1;
+      if (!more) break;
       v = vn;
-      vn = m ? __builtin_ctz(m) : v;
-      wload(vn, wa);
-      aload(vn, aa);
+      kc = kn;
+      advance(vn, kn);
+      wload(vn, kn, wa);
+      aload(vn, kn, aa);
       compute(v, wb, ab);
-      if (!m) break;
-      m &= m - 1;
+      if (!more) break;
       v = vn;
+      kc = kn;
     }
   }
 
@@ -1121,15 +1141,18 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
   }
 }
 
-// Halo shapes per input width (rows per tile, halo rows at most, groups and channel tiles per wavefront). Only
-// Ci = 64 is served: at Ci = 128 (C5's children, 128-row windows of 256-byte rows) the kernel was correct but
-// slower than the gathering kernel (1.11 vs 0.91 ms) -- the children's 16-row masks are nearly random, so the
-// MFMA work (2x the active pairs and more) dominates once the gathers are gone.
+// Halo shapes per input width (rows per tile, halo rows at most, groups and channel tiles per wavefront). Ci = 64
+// by default; Ci = 128 on request (SPCONV_HALO128, see halo128_enabled for why it is not the default).
 template <int S>
 struct HaloShape;
 template <>
 struct HaloShape<2> {  // Ci = 64: 256-row windows, up to 512 halo rows (80 KB of LDS, two workgroups per CU)
   static constexpr int B = 256, UM = 512, G = 4, T = 4, OCC = 2;
+};
+template <>
+struct HaloShape<4> {  // Ci = 128: 128-row windows, up to 256 halo rows of 256 bytes (73 KB, two workgroups per CU);
+                       // wavefronts of 64 rows x 32 channels
+  static constexpr int B = 128, UM = 256, G = 4, T = 2, OCC = 2;
 };
 
 template <bool F16, int S>
@@ -1961,7 +1984,7 @@ void launch(ConvArgs a) {
 template <bool F16>
 void dispatch(const SpConvCfg& cfg, ConvArgs a) {
   // The fp16-compatible epilogue (EPI_F16_COMPAT) runs in every kernel: store_row8 applies it.
-  if (a.hrows) return launch_halo<F16, 2>(a);
+  if (a.hrows) return a.Ci == 64 ? launch_halo<F16, 2>(a) : launch_halo<F16, 4>(a);
   if (a.Co == 64 && a.Ci <= 128) {
     switch (a.Ci / 32) {
       case 1: return launch_narrow<F16, 1, 4>(a);
@@ -2013,6 +2036,14 @@ bool halo_enabled() {
     return !(e && e[0] && e[0] != '0');
   }();
   return on;
+}
+// Ci = 128 -> 64 takes the halo kernel only when SPCONV_HALO128 is set (read per call). Measured on C5's children
+// (same box): 1.13 ms against 0.99 for the gathering kernel. The halo removes the gather misses, but a wavefront
+// pair of 64 rows loads the whole 442 KB weight tensor from L2 (7.4 GB per launch, the per-CU load path's largest
+// stream), and 128-row windows leave 16-row groups at 3.2x the active pairs (2.1x in 65536-row windows).
+bool halo128_enabled() {
+  const char* e = getenv("SPCONV_HALO128");
+  return halo_enabled() && e && e[0] && e[0] != '0';
 }
 
 // x: the conv input [N,Ci], or with row_map the source rows [M,Ci] read through row_map >> shift
@@ -2091,6 +2122,9 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   const SpConvCache::HaloTable* ht = nullptr;
   if (Co == 64 && Ci == 64 && halo_enabled()) {
     ht = &c.halo_table(HaloShape<2>::B, HaloShape<2>::UM);
+    if (!ht->ok) ht = nullptr;
+  } else if (Co == 64 && Ci == 128 && halo128_enabled()) {
+    ht = &c.halo_table(HaloShape<4>::B, HaloShape<4>::UM);
     if (!ht->ok) ht = nullptr;
   }
   if (ht) {  // halo kernel: narrow weight order, the tile's distinct neighbour rows copied to LDS once
@@ -2172,8 +2206,8 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       map_table_rows(ht->spill.tbl, *row_map, shift, M, mtbl);
       sa.tbl = mtbl.ptr<uint32_t>();
     }
-    if (x.dt == F16) launch_narrow<true, 2, 4>(sa);
-    else launch_narrow<false, 2, 4>(sa);
+    if (Ci == 64) x.dt == F16 ? launch_narrow<true, 2, 4>(sa) : launch_narrow<false, 2, 4>(sa);
+    else x.dt == F16 ? launch_narrow<true, 4, 4>(sa) : launch_narrow<false, 4, 4>(sa);
     CK(hipGetLastError());
   }
 }

@@ -1043,6 +1043,7 @@ const SpConvCache::HaloTable& SpConvCache::halo_table(int B, int UM) {
                                               flag.ptr<int32_t>());
   };
   if (B == 256 && UM == 512) go(k_halo_build<256, 512>);
+  else if (B == 128 && UM == 256) go(k_halo_build<128, 256>);
   else REQ(false, "no halo builder for B=%d UM=%d", B, UM);
   CK(hipGetLastError());
   const auto fl = to_host_vec<int32_t>(flag);  // one host sync per cache and shape
