@@ -953,6 +953,17 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
   const int wr = wv / WC, wc = wv % WC;
   const int N = a.N;
+  // halo row ids of this wavefront's DMA units, loaded together with the tile's row count instead of after it
+  // (slots past the count hold -1, so no load depends on it): one memory round trip fewer before the DMA
+  // (C4 prologue 9.7 -> 3.6 us per tile, kernel 0.77 -> 0.64 ms)
+  constexpr int NINS = ((UM * RU + 63) / 64 + 3) / 4;  // DMA instructions per wavefront for a full halo
+  const int32_t* hr = a.hrows + (size_t)tile * UM;
+  int hrow[NINS];
+#pragma unroll
+  for (int k = 0; k < NINS; k++) {
+    const int u = ((k * 4 + wv) * 64 + lane) / RU;
+    hrow[k] = u < UM ? hr[u] : -1;
+  }
   const int U = __builtin_amdgcn_readfirstlane(a.hcount[tile]);
   if (U < 0) return;  // a spill tile (more distinct rows than UM): the gathering kernel computes its rows
 
@@ -967,11 +978,13 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
                                                  16, (uint32_t)u * 16u, 0, 0, 0);
     }
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
-    const int32_t* hr = a.hrows + (size_t)tile * UM;
     const int nins = (U * RU + 63) / 64;  // wavefront instructions of 64 x 16 bytes (64 / RU halo rows each)
-    for (int j = wv; j < nins; j += 4) {
+#pragma unroll
+    for (int k = 0; k < NINS; k++) {
+      const int j = k * 4 + wv;
+      if (j >= nins) break;
       const int unit = j * 64 + lane, u = unit / RU, c = unit % RU;
-      int h = u < U ? hr[u] : -1;
+      int h = hrow[k];
       if (a.rmap && h >= 0) {  // gathered conv: the halo row is row_map[h] >> shift of the source matrix
         const uint32_t q = (uint32_t)a.rmap[h] >> a.rshift;
         h = q < (uint32_t)a.rmax ? (int)q : -1;

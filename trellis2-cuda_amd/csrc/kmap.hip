@@ -994,6 +994,7 @@ __global__ void __launch_bounds__(B) k_halo_build(const uint32_t* __restrict__ n
       base++;
     }
   }
+  for (int u = U + tid; u < UM; u += B) rows[t * UM + u] = -1;  // unused slots: the conv loads them unconditionally
   __syncthreads();
 #pragma unroll
   for (int v = 0; v < 27; v++) {
