@@ -883,8 +883,6 @@ uint32_t* noalloc_scratch() {
 
 i64 subdivide_noalloc_max_parents() { return kNoAllocMaxParents; }
 
-void subdivide_noalloc_init() { (void)noalloc_scratch(); }
-
 void subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, i64 n, int32_t* child_coords, int32_t* src,
                        i64* m_dev) {
   REQ(n >= 0 && n <= kNoAllocMaxParents, "subdivide_noalloc: %lld parents, at most %lld", (long long)n,

@@ -184,10 +184,9 @@ struct UpsampleLevel {
 UpsampleLevel subdivide_build(const Tensor& coords, const Tensor& logits_f16, int W, int H, int D,
                               int32_t* coords_out = nullptr, int32_t* src_out = nullptr);
 // The same children written into caller buffers of >= 8n rows, the count into device memory (*m_dev, int64), with no
-// allocation and no host sync: its scratch is a static device array (see kmap.hip), so n <= the maximum below and
-// concurrent calls on one GPU race. init() looks up the array's device address on the current device.
+// allocation and no host sync: its scratch is a static device array whose device address is looked up on a
+// device's first call, so n <= the maximum below and concurrent calls on one GPU race.
 i64 subdivide_noalloc_max_parents();
-void subdivide_noalloc_init();
 void subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, i64 n, int32_t* child_coords, int32_t* src,
                        i64* m_dev);
 

@@ -89,6 +89,7 @@ void subm_conv_replay(const Tensor& x, const Tensor& w, const Tensor* b, const T
       "cfg B1=%d BK=%d S=%d with Ci=%d (B1, BK multiples of 32, Ci %% BK == 0, 1 <= S <= 64)", cfg.B1, cfg.BK, cfg.S,
       Ci);
   REQ(Co % 32 == 0, "Co=%d must be a multiple of 32", Co);
+  REQ(((uintptr_t)x.p | (uintptr_t)w.p) % 16 == 0, "x and w must be 16-byte aligned");
   REQ(out.dim() == 2 && out.size(0) == N && out.size(1) == Co, "out must be [N,Co]");
   if (residual) REQ(residual->numel() == (i64)N * Co, "residual must be [N,Co]");
   if (cfg.S == 1) {  // FlexGEMM's unsplit kernel: f16(acc), then the fp16 bias add
