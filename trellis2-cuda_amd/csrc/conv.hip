@@ -746,6 +746,23 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   }
   wait_vmcnt<0>();  // this lane's table DMA has landed (the barrier below covers the other lanes)
   __syncthreads();
+  if (a.rmap) {  // gathered conv: the tile's neighbour rows become source rows row_map[r] >> shift (EMPTY past rmax)
+    constexpr int NE = BM * SR, PER = (NE + NT - 1) / NT;
+    uint32_t mv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int e = k * NT + tid;
+      const uint32_t r = e < NE ? srcT[e] : EMPTY;
+      mv[k] = r != EMPTY ? (uint32_t)a.rmap[r] : EMPTY;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int e = k * NT + tid;
+      const uint32_t q = mv[k] == EMPTY ? EMPTY : mv[k] >> a.rshift;
+      if (e < NE) srcT[e] = q < (uint32_t)a.rmax ? q : EMPTY;
+    }
+    __syncthreads();
+  }
   uint32_t mask = 0;
 #pragma unroll
   for (int i = 0; i < BM / 16; i++) mask |= gmask[i];
@@ -2170,11 +2187,15 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     k_pack_w_narrow<<<dim3(Ci / 32, Co / 16, 27), 64, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
     a.w = wpack.ptr<uint16_t>();
     const SpConvCache::RowTable& rt = c.row_table(16);
-    if (row_map) mtbl = c.mapped_table(16, *row_map, shift, M);
     a.order = rt.order.ptr<int32_t>();
-    a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
+    a.tbl = rt.tbl.ptr<uint32_t>();
     a.gs = rt.gs.ptr<int32_t>();
     a.tbl_bytes = (uint32_t)rt.tbl.bytes();
+    if (row_map) {  // the kernel maps each tile's neighbour rows in its prologue (no mapped copy of the table)
+      a.rmap = row_map->ptr<int32_t>();
+      a.rshift = shift;
+      a.rmax = (int)std::min<i64>(M, INT32_MAX);
+    }
   } else if (Co % 256 == 0 && Ci % 64 == 0 && w256_enabled()) {  // 256 x 256 tiles: 4 KB weight blocks
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w256<<<dim3(Ci / 64, 27, Co / 32), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Ci);
