@@ -1200,12 +1200,12 @@ void launch_halo(ConvArgs a) {
 }
 
 template <bool F16, int S, int T>
-void launch_narrow(ConvArgs a) {
+void launch_narrow(ConvArgs a, hipStream_t st = stream()) {
   constexpr int G = S <= 2 ? 4 : 2;  // 16-row groups per wavefront: keeps two wavefronts per SIMD at Ci = 128
   a.tiles_m = cdiv(a.N, 4 * 16 * G);
   a.tiles_n = 1;
   a.grid = (a.tiles_m + 7) / 8 * 8;
-  k_conv_narrow<F16, S, T, G><<<a.grid, 256, 0, stream()>>>(a);
+  k_conv_narrow<F16, S, T, G><<<a.grid, 256, 0, st>>>(a);
 }
 
 // Wide-channel kernel, BM sorted rows x 256 channels per workgroup (4 wavefronts, each all BM rows x 64 channels =
@@ -2064,6 +2064,26 @@ __global__ void k_gather_rows(const u32x4* __restrict__ x, i64 m, int units, con
   out[q] = r < (uint64_t)m ? x[(i64)r * units + (q - i * units)] : u32x4{0, 0, 0, 0};
 }
 
+// A second stream per device (default priority, like the library stream) with a fork and a join event, for the
+// spill tiles' gathering kernel, which runs beside the halo kernel. Created on first use, kept until the process ends.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+SideStream& side_stream() {
+  static SideStream ss[64];
+  int dev = 0;
+  CK(hipGetDevice(&dev));
+  REQ(dev >= 0 && dev < 64, "device %d", dev);
+  SideStream& r = ss[dev];
+  if (!r.s) {
+    CK(hipStreamCreateWithFlags(&r.s, hipStreamNonBlocking));
+    CK(hipEventCreateWithFlags(&r.fork, hipEventDisableTiming));
+    CK(hipEventCreateWithFlags(&r.join, hipEventDisableTiming));
+  }
+  return r;
+}
+
 // The halo kernel serves Ci = Co = 64 unless SPCONV_NO_HALO is set (then the gathering narrow kernel does).
 bool halo_enabled() {
   static const bool on = [] {
@@ -2225,10 +2245,10 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     }
   }
   REQ(!skip || (ht && ht->spill_n == 0), "the fused skip residual needs the halo kernel with no spill tiles");
-  if (x.dt == F16) dispatch<true>(cfg, a);
-  else dispatch<false>(cfg, a);
-  CK(hipGetLastError());
-  if (ht && ht->spill_n > 0) {  // the halo kernel skipped the spill tiles: their positions go to the gathering kernel
+  if (ht && ht->spill_n > 0) {
+    // The halo kernel skips the spill tiles; their positions go to the gathering kernel. It runs on a second stream
+    // beside the halo kernel (a few tiles of long latency; after it, it added ~36 us to C4's 0.64 ms): fork after
+    // everything both kernels read is queued on the library stream, join before anything later on it.
     ConvArgs sa = a;
     sa.hrows = nullptr;
     sa.hcount = nullptr;
@@ -2245,10 +2265,22 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       map_table_rows(ht->spill.tbl, *row_map, shift, M, mtbl);
       sa.tbl = mtbl.ptr<uint32_t>();
     }
-    if (Ci == 64) x.dt == F16 ? launch_narrow<true, 2, 4>(sa) : launch_narrow<false, 2, 4>(sa);
-    else x.dt == F16 ? launch_narrow<true, 4, 4>(sa) : launch_narrow<false, 4, 4>(sa);
+    SideStream& ss = side_stream();
+    CK(hipEventRecord(ss.fork, stream()));
+    CK(hipStreamWaitEvent(ss.s, ss.fork, 0));
+    if (Ci == 64) x.dt == F16 ? launch_narrow<true, 2, 4>(sa, ss.s) : launch_narrow<false, 2, 4>(sa, ss.s);
+    else x.dt == F16 ? launch_narrow<true, 4, 4>(sa, ss.s) : launch_narrow<false, 4, 4>(sa, ss.s);
     CK(hipGetLastError());
+    CK(hipEventRecord(ss.join, ss.s));
+    if (x.dt == F16) dispatch<true>(cfg, a);
+    else dispatch<false>(cfg, a);
+    CK(hipGetLastError());
+    CK(hipStreamWaitEvent(stream(), ss.join, 0));
+    return;
   }
+  if (x.dt == F16) dispatch<true>(cfg, a);
+  else dispatch<false>(cfg, a);
+  CK(hipGetLastError());
 }
 
 void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, const Tensor& x_skip,
