@@ -292,6 +292,9 @@ def measure(name, args, torch, np, sp, W, cpu, want_cpu, cpu_seconds, extras):
         def half_fused_skip():
             sp.subm_conv_skip(sp.gather_ln_act(h1, src, 0), w2, b2, cc, xp, src, out=y2)
 
+        def half_one_kernel():  # gather + LayerNorm + SiLU + conv2 + skip in the halo kernel
+            sp.subm_conv_preln(h1, w2, b2, cc, src, 0, None, None, 1e-6, sp.ACT_SILU, x_skip=xp, skip_src=src, out=y2)
+
         def torch_preact():
             torch.nn.functional.silu(torch.nn.functional.layer_norm(h1[src.long()].float(), (co2,), eps=1e-6)).to(
                 torch.bfloat16)
@@ -299,6 +302,7 @@ def measure(name, args, torch, np, sp, W, cpu, want_cpu, cpu_seconds, extras):
             "children": len(ch), "Co": co2,
             "gather_ln_silu_then_conv_ms": round(timed(half_gathered_rows, 10), 4),
             "gather_ln_silu_then_conv_skip_fused_ms": round(timed(half_fused_skip, 10), 4),
+            "preln_conv_skip_one_kernel_ms": round(timed(half_one_kernel, 10), 4),
             "gather_ln_silu_ms": round(timed(lambda: sp.gather_ln_act(h1, src, 0), 20), 4),
             "torch_gather_ln_silu_ms": round(timed(torch_preact, 20), 4),
             "add_skip_ms": round(timed(lambda: sp.add_skip(y2, xp, src), 20), 4)}

@@ -149,6 +149,20 @@ int spc_subm_conv_skip(const void* x, const void* w, const void* b, int dtype, i
                        const void* x_skip, int64_t n_skip, int Cin, const int32_t* src, int64_t N, int Ci, int Co,
                        spc_cache* c, void* out);
 
+/* Conv of pre-activated rows: x = pre_act(LayerNorm(x_src[row_map[i] >> shift]) * gamma + beta) (fp32 statistics,
+ * one rounding; row_map NULL: the rows of x_src, M == N), out = act(conv(x, w) + b), plus, when x_skip / skip_src
+ * are given, the skip of spc_subm_conv_skip. x_src [M,Ci], w [Co,27,Ci], x_skip [n_skip,Cin], out [N,Co]: one
+ * 16-bit `dtype`; gamma, beta float [Ci] or NULL; pre_act SPC_ACT_NONE / SPC_ACT_SILU. Runs spc_gather_ln_act's
+ * pass and then the conv; with the environment switch SPCONV_PRELN_FUSED=1, 64 -> 64 convs whose schedule has no
+ * spill tiles run as one kernel (the pre-activation applied to each tile's distinct input rows in LDS; slower on
+ * the shapes measured) -- the same bits either way.
+ * Replaces: k_gather_rows + layer_norm + act_ SILU + subm_conv (+ k_add_skip) of SDecoder::up (src/sdec.cu:78-84,
+ * src/ops.cu:30-82). */
+int spc_subm_conv_preln(const void* x_src, int64_t M, const int32_t* row_map, int shift, const float* gamma,
+                        const float* beta, float eps, int pre_act, const void* w, const void* b, int dtype, int b_dtype,
+                        int act, const void* x_skip, int64_t n_skip, int Cin, const int32_t* skip_src, int64_t N,
+                        int Ci, int Co, spc_cache* c, void* out);
+
 /* Skip connection of the upsample block, in place: h[i,c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep] with
  * rep = Co / (Cin/8), the fp32 sum rounded once to `dtype` (bit-identical to the reference); h [m,Co], x [n,Cin],
  * both SPC_F16 or SPC_BF16, 16-byte aligned; Cin % 8 == 0, Co % 8 == 0, Co % (Cin/8) == 0. src entries outside

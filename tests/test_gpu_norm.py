@@ -197,3 +197,71 @@ def test_conv_skip(gpu, Cin, Ci):
         rel = np.linalg.norm(yr - ref) / np.linalg.norm(ref)
         err = np.abs(yr - ref)
         assert rel <= 3e-3 and np.all(err <= np.maximum(2e-2, ulp(ref, torch.bfloat16))), (act, rel, err.max())
+
+
+@pytest.mark.parametrize("fused", ["1", "0"])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_conv_preln(gpu, monkeypatch, dt, fused):
+    """subm_conv_preln (fused = 1: gather + LayerNorm + SiLU + conv + skip in the halo kernel; 0: the two-pass
+    default) equals gather_ln_act followed by
+    subm_conv_skip / subm_conv_fused bit for bit: with and without the skip, the affine terms and the SiLU, through
+    the c2s map (shift 0, an upsample block's h1 sub-rows), through a shift-3 map, with no map, and with map entries
+    outside the source (those rows are act(beta), as gather_ln_act makes them). The composition itself is checked
+    against torch + the oracle in test_upsample_block."""
+    from spconv_amd import workloads as W
+    par = W.shell_coords(W.CONFIGS["c1"])
+    n, Co = len(par), 64
+    ch, src = sp.subdivide(torch.from_numpy(par).to(gpu),
+                           torch.from_numpy(W.keep_logits(n, 0.35, 6).view(np.int16)).to(gpu).view(torch.float16))
+    m = len(ch)
+    monkeypatch.setenv("SPCONV_PRELN_FUSED", fused)
+    print(f"preln case dt={dt} fused={fused} parents={n} children={m}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    h1 = (torch.randn((8 * n, Co), generator=g) * 1.5 + 0.3).to(dt).to(gpu)  # h1 sub-rows, read through src
+    hp = torch.randn((n, Co), generator=g).to(dt).to(gpu)  # parent rows, read through src >> 3
+    hc = torch.randn((m, Co), generator=g).to(dt).to(gpu)  # child rows, no map
+    xs = torch.randn((n, 128), generator=g).to(dt).to(gpu)
+    w, b = W.conv_params(W.Config("t", 0, 0, (0, 0), False, 0, Co, Co, "bf16", "", 23))
+    wg, bg = torch.from_numpy(w).to(dt).to(gpu), torch.from_numpy(b).to(gpu)
+    gamma = (torch.rand(Co, generator=g) + 0.5).to(gpu)
+    beta = (torch.randn(Co, generator=g) * 0.2).to(gpu)
+    bad = src.clone()
+    bad[::97] = 8 * n + 5  # outside the source rows
+    cache = sp.build_neighbors(ch.contiguous())
+    cases = [(h1, src, 0), (hp, src, 3), (hc, None, 0), (h1, bad, 0)]
+    for k, (xsrc, rmap, shift) in enumerate(cases):
+        for affine in (False, True):
+            for pre_act in (0, 1):
+                ga, be = (gamma, beta) if affine else (None, None)
+                h = sp.gather_ln_act(xsrc, rmap, shift, ga, be, 1e-6, pre_act)
+                ref = sp.subm_conv_skip(h, wg, bg, cache, xs, src, act=1)
+                y = sp.subm_conv_preln(xsrc, wg, bg, cache, rmap, shift, ga, be, 1e-6, pre_act, act=1, x_skip=xs,
+                                       skip_src=src)
+                assert torch.equal(y, ref), (k, affine, pre_act, "skip")
+                ref2 = sp.subm_conv_fused(h, wg, bg, cache, act=0)
+                y2 = sp.subm_conv_preln(xsrc, wg, bg, cache, rmap, shift, ga, be, 1e-6, pre_act, act=0)
+                assert torch.equal(y2, ref2), (k, affine, pre_act, "no skip")
+
+
+def test_conv_preln_spill_and_ci128(gpu, monkeypatch):
+    """subm_conv_preln with the one-kernel form requested, on a cache with spill tiles (it takes gather_ln_act + the
+    conv) and at Ci = 128 on the opt-in 128-channel halo kernel and on the gathering kernel: bit for bit the
+    composition."""
+    from test_gpu_conv import mixed_spill_coords
+    c = mixed_spill_coords()
+    n = len(c)
+    print(f"preln spill case rows={n}", flush=True)
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    g = torch.Generator().manual_seed(5)
+    monkeypatch.setenv("SPCONV_PRELN_FUSED", "1")
+    for Ci in (64, 128):
+        x = (torch.randn((n, Ci), generator=g) + 0.2).to(torch.bfloat16).to(gpu)
+        w = (torch.randn((64, 27, Ci), generator=g) / (27 * Ci) ** 0.5).to(torch.bfloat16).to(gpu)
+        b = (torch.randn(64, generator=g) * 0.1).to(gpu)
+        gamma = (torch.rand(Ci, generator=g) + 0.5).to(gpu)
+        beta = (torch.randn(Ci, generator=g) * 0.1).to(gpu)
+        for mode in ("0", "1"):
+            monkeypatch.setenv("SPCONV_HALO128", mode)
+            ref = sp.subm_conv_fused(sp.gather_ln_act(x, None, 0, gamma, beta, 1e-5, 1), w, b, cache, act=1)
+            y = sp.subm_conv_preln(x, w, b, cache, None, 0, gamma, beta, 1e-5, 1, act=1)
+            assert torch.equal(y, ref), (Ci, mode)

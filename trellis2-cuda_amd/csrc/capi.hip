@@ -212,6 +212,37 @@ SPC_API int spc_subm_conv_skip(const void* x, const void* w, const void* b, int 
   });
 }
 
+SPC_API int spc_subm_conv_preln(const void* x_src, int64_t M, const int32_t* row_map, int shift, const float* gamma,
+                                const float* beta, float eps, int pre_act, const void* w, const void* b, int dtype,
+                                int b_dtype, int act, const void* x_skip, int64_t n_skip, int Cin,
+                                const int32_t* skip_src, int64_t N, int Ci, int Co, spc_cache* c, void* out) {
+  return guarded([&] {
+    REQ(c, "cache is null");
+    REQ(N == c->c.N, "N=%lld but the cache has %d rows", (long long)N, c->c.N);
+    REQ(M >= 0 && Ci > 0 && Co > 0 && n_skip >= 0, "M=%lld Ci=%d Co=%d n_skip=%lld", (long long)M, Ci, Co,
+        (long long)n_skip);
+    REQ((x_skip == nullptr) == (skip_src == nullptr), "x_skip and skip_src go together");
+    DT dt = float_dt(dtype, "x_src/w/x_skip/out");
+    REQ(dt != F32, "x_src/w/x_skip/out must be fp16 or bf16");
+    if (N == 0) return;
+    REQ(row_map || M == N, "without a row map M (%lld) must equal N (%lld)", (long long)M, (long long)N);
+    REQ(x_src && w && out && M > 0, "null x_src/w/out or M = 0");
+    REQ(!x_skip || (Cin > 0 && n_skip > 0), "x_skip needs Cin > 0 and n_skip > 0");
+    Tensor tx = borrow(x_src, {M, Ci}, dt), tw = borrow(w, {Co, 27, Ci}, dt), to = borrow(out, {N, Co}, dt);
+    Tensor tm, tg, tbt, tb, ts, tsrc;
+    if (row_map) tm = borrow(row_map, {N}, I32);
+    if (gamma) tg = borrow(gamma, {Ci}, F32);
+    if (beta) tbt = borrow(beta, {Ci}, F32);
+    if (b) tb = borrow(b, {Co}, float_dt(b_dtype, "bias"));
+    if (x_skip) {
+      ts = borrow(x_skip, {n_skip, Cin}, dt);
+      tsrc = borrow(skip_src, {N}, I32);
+    }
+    subm_conv_preln(tx, row_map ? &tm : nullptr, shift, gamma ? &tg : nullptr, beta ? &tbt : nullptr, eps, pre_act,
+                    tw, b ? &tb : nullptr, act, x_skip ? &ts : nullptr, x_skip ? &tsrc : nullptr, c->c, to);
+  });
+}
+
 SPC_API int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, int Co, int64_t n, int Cin,
                          int dtype) {
   return guarded([&] {

@@ -17,6 +17,7 @@
 // tile adjacent in time.
 #include <utility>
 
+#include "lnact.h"
 #include "spconv.h"
 
 
@@ -117,6 +118,12 @@ struct ConvArgs {
   const int32_t* skip_src;
   int skip_cin, skip_rep;
   uint32_t skip_bytes, skip_n;
+  // pre-activation of the input rows (halo kernel only, ln_on): each halo row becomes act(LayerNorm(row) * ln_gamma
+  // + ln_beta) before the K loop, ln_act = ACT_NONE / ACT_SILU, gamma / beta f32 [Ci] or null
+  const float* ln_gamma;
+  const float* ln_beta;
+  float ln_eps;
+  int ln_act, ln_on;
   int N, Ci, Co, res_dt, out_dt, act;
   int tiles_m, tiles_n, grid;
   uint32_t x_bytes, w_bytes, nbr_bytes, res_bytes, out_bytes, tbl_bytes;
@@ -1019,6 +1026,31 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
     if (tid < B / 16) gmL[tid] = a.hgm[(size_t)tile * (B / 16) + tid];
   }
   wait_vmcnt<0>();
+  if (a.ln_on) {
+    // pre-activation of the halo rows in place: RU lanes per row, lane c holding the row's logical chunk c (stored
+    // at c ^ hsw(u)), as gather_ln_act holds it, so the result is the same bits. Rows past the count are padding;
+    // the zero row stays zero (an EMPTY neighbour), while a row whose source is out of range holds zeros and
+    // becomes act(beta), as gather_ln_act makes it. Every lane takes part in the shuffles. Thread tid's unit
+    // base + tid is the one its own lane DMA'd (instruction k * 4 + wv), and a row's units come from one DMA
+    // instruction of the same wavefront, so this wavefront's wait above is enough: one barrier, after.
+    for (int base = 0; base < U * RU; base += 256) {
+      const int unit = base + tid, u = unit / RU, c = unit % RU;
+      const bool live = u < U;
+      u32x4* p = &halo[(live ? u : 0) * RU + (c ^ hsw(live ? u : 0))];
+      const u32x4 q = live ? *p : u32x4{0, 0, 0, 0};
+      float v[1][8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[0][j] = lnact_h2f((uint16_t)(q[j >> 1] >> ((j & 1) * 16)), !F16);
+      float mean, rstd;
+      ln_stats<RU, 1>(v, CI, a.ln_eps, mean, rstd);
+      float o[8];
+      ln_out8(v[0], mean, rstd, a.ln_gamma ? a.ln_gamma + c * 8 : nullptr, a.ln_beta ? a.ln_beta + c * 8 : nullptr,
+              a.ln_act == ACT_SILU, o);
+      if (live)
+        *p = u32x4{lnact_pack2(o[0], o[1], !F16), lnact_pack2(o[2], o[3], !F16), lnact_pack2(o[4], o[5], !F16),
+                   lnact_pack2(o[6], o[7], !F16)};
+    }
+  }
   __syncthreads();
 
   // epilogue layout (16-byte row segments, LPR lanes per row) and the output rows, fetched now for later
@@ -2106,8 +2138,15 @@ struct SkipRes {  // skip residual of the upsample block (see ConvArgs::skip_*)
   const Tensor* x;
   const Tensor* src;
 };
+struct PreLN {  // pre-activation of the input rows (see ConvArgs::ln_*); only with the halo kernel
+  const Tensor* gamma;
+  const Tensor* beta;
+  float eps;
+  int act;
+};
 void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& w, const Tensor* b,
-               const Tensor* residual, int act, SpConvCache& c, Tensor& out, const SkipRes* skip = nullptr) {
+               const Tensor* residual, int act, SpConvCache& c, Tensor& out, const SkipRes* skip = nullptr,
+               const PreLN* ln = nullptr) {
   REQ(x.dim() == 2 && w.dim() == 3, "x must be [N,Ci], w [Co,27,Ci]");
   const int N = row_map ? c.N : (int)x.size(0), Ci = (int)x.size(1), Co = (int)w.size(0);
   const i64 M = x.size(0);
@@ -2245,6 +2284,14 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     }
   }
   REQ(!skip || (ht && ht->spill_n == 0), "the fused skip residual needs the halo kernel with no spill tiles");
+  REQ(!ln || (ht && ht->spill_n == 0), "the fused pre-activation needs the halo kernel with no spill tiles");
+  if (ln) {
+    a.ln_on = 1;
+    a.ln_gamma = ln->gamma ? ln->gamma->ptr<float>() : nullptr;
+    a.ln_beta = ln->beta ? ln->beta->ptr<float>() : nullptr;
+    a.ln_eps = ln->eps;
+    a.ln_act = ln->act;
+  }
   if (ht && ht->spill_n > 0) {
     // The halo kernel skips the spill tiles; their positions go to the gathering kernel. It runs on a second stream
     // beside the halo kernel (a few tiles of long latency; after it, it added ~36 us to C4's 0.64 ms): fork after
@@ -2330,6 +2377,66 @@ void subm_conv_gathered(const Tensor& x_src, const Tensor& row_map, int shift, c
                                                                    row_map.ptr<int32_t>(), shift, c.N, (u32x4*)xg.p);
   CK(hipGetLastError());
   conv_impl(xg, nullptr, 0, w, b, residual, act, c, out);
+}
+
+// Conv of pre-activated rows: x = act_pre(LayerNorm(x_src[row_map >> shift]) * gamma + beta), then the conv with
+// bias and act, plus the upsample block's skip residual when x_skip / skip_src are given (as subm_conv_skip).
+// By default gather_ln_act writes x and the conv (and skip) run on it. With SPCONV_PRELN_FUSED set, and when the
+// halo kernel serves the cache with no spill tiles, the pre-activation runs instead on each tile's halo rows in LDS
+// before the K loop (one kernel for gather + LayerNorm + SiLU + conv + skip). Both give the same bits. The one
+// kernel is the slower form (C5 children, 64 -> 64 with the skip: 0.694 ms against 0.620 for the two passes): the
+// LayerNorm and SiLU of ~1.4 halo rows per output row sit on every tile's path between its halo DMA and its K loop.
+bool preln_fused_enabled() {
+  const char* e = getenv("SPCONV_PRELN_FUSED");
+  return e && e[0] && e[0] != '0';
+}
+
+void subm_conv_preln(const Tensor& x_src, const Tensor* row_map, int shift, const Tensor* gamma, const Tensor* beta,
+                     float eps, int pre_act, const Tensor& w, const Tensor* b, int act, const Tensor* x_skip,
+                     const Tensor* skip_src, SpConvCache& c, Tensor& out) {
+  REQ(x_src.dim() == 2 && (x_src.dt == BF16 || x_src.dt == F16) && w.dim() == 3, "x_src bf16/fp16 [M,Ci], w [Co,27,Ci]");
+  REQ(pre_act == ACT_NONE || pre_act == ACT_SILU, "pre_act=%d", pre_act);
+  REQ(!(act & EPI_F16_COMPAT), "no fp16-compatible epilogue with the fused pre-activation");
+  REQ((x_skip == nullptr) == (skip_src == nullptr), "x_skip and skip_src go together");
+  const int Ci = (int)x_src.size(1), Co = (int)w.size(0);
+  if (row_map) {
+    REQ(row_map->dt == I32 && row_map->numel() == c.N, "row_map must be int32 [%d]", c.N);
+    REQ(shift >= 0 && shift < 31, "shift=%d", shift);
+  } else {
+    REQ(x_src.size(0) == c.N, "without a row map x_src must have the cache's %d rows", c.N);
+  }
+  if (gamma) REQ(gamma->dt == F32 && gamma->numel() == Ci, "gamma must be f32 [%d]", Ci);
+  if (beta) REQ(beta->dt == F32 && beta->numel() == Ci, "beta must be f32 [%d]", Ci);
+  if (x_skip) {
+    REQ(skip_src->dt == I32 && skip_src->numel() == c.N, "skip_src must be int32 [%d]", c.N);
+    REQ(x_skip->dim() == 2 && x_skip->dt == out.dt && out.dt == x_src.dt, "x_skip, x_src and out: one 16-bit dtype");
+  }
+  if (c.N == 0) return;
+  bool fused = preln_fused_enabled() && Co == 64 && ((Ci == 64 && halo_enabled()) || (Ci == 128 && halo128_enabled()));
+  if (fused) {
+    const SpConvCache::HaloTable& ht =
+        Ci == 64 ? c.halo_table(HaloShape<2>::B, HaloShape<2>::UM) : c.halo_table(HaloShape<4>::B, HaloShape<4>::UM);
+    fused = ht.ok && ht.spill_n == 0;
+  }
+  if (fused) {
+    const PreLN pl{gamma, beta, eps, pre_act};
+    if (x_skip) {
+      const SkipRes sk{x_skip, skip_src};
+      const int Cin = (int)x_skip->size(1);
+      REQ(Cin % 64 == 0 && Co % (Cin / 8) == 0 && ((Co / (Cin / 8)) & (Co / (Cin / 8) - 1)) == 0,
+          "Cin=%d Co=%d: need Cin %% 64 == 0 and Co / (Cin/8) a power of two", Cin, Co);
+      REQ((uint64_t)x_skip->bytes() <= kMaxBufferBytes && ((uintptr_t)x_skip->p % 16) == 0,
+          "x_skip too large / unaligned");
+      conv_impl(x_src, row_map, shift, w, b, nullptr, act, c, out, &sk, &pl);
+    } else {
+      conv_impl(x_src, row_map, shift, w, b, nullptr, act, c, out, nullptr, &pl);
+    }
+    return;
+  }
+  Tensor h = empty({(i64)c.N, Ci}, x_src.dt);
+  gather_ln_act(x_src, row_map, shift, gamma, beta, eps, pre_act, h);
+  if (x_skip) subm_conv_skip(h, w, b, act, *x_skip, *skip_src, c, out);
+  else subm_conv_fused(h, w, b, nullptr, act, c, out);
 }
 
 Tensor subm_conv(const Tensor& x, const Tensor& w, const Tensor* b, SpConvCache& c) {

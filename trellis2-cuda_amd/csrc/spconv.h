@@ -157,6 +157,17 @@ void convnext_mlp(const Tensor& h, const Tensor& x, const Tensor* gamma, const T
 void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, const Tensor& x_skip,
                     const Tensor& src, SpConvCache& c, Tensor& out);
 
+// Conv of pre-activated rows (the upsample block's norm2 + SiLU + conv2 + skip, reference src/sdec.cu:78-84, or
+// any LayerNorm -> act -> conv): x = act_pre(LayerNorm(x_src[row_map >> shift]) * gamma + beta) (row_map null: the
+// rows of x_src, which then has the cache's rows), out = act(conv(x, w) + b) [+ the skip of subm_conv_skip when
+// x_skip / skip_src are given]: gather_ln_act and then the conv; with SPCONV_PRELN_FUSED set, 64-output-channel
+// convs served by the halo kernel without spill tiles run it as one kernel instead (the pre-activation applied to
+// each tile's halo rows in LDS; slower, see conv.hip). Same bits either way. x_src, w, x_skip, out: one 16-bit
+// dtype; gamma / beta f32 [Ci] or null.
+void subm_conv_preln(const Tensor& x_src, const Tensor* row_map, int shift, const Tensor* gamma, const Tensor* beta,
+                     float eps, int pre_act, const Tensor& w, const Tensor* b, int act, const Tensor* x_skip,
+                     const Tensor* skip_src, SpConvCache& c, Tensor& out);
+
 // Skip connection of the upsample block, in place (reference k_add_skip, src/sdec.cu:38-43):
 // h[i, c] += x[src[i] >> 3, (src[i] & 7) * Cin/8 + c / rep], rep = Co / (Cin/8), fp32 sum rounded once (bit-identical
 // to the reference). h [m,Co] and x [n,Cin] of one dtype (fp16/bf16); entries of src outside x leave the row.

@@ -5,22 +5,15 @@
 // Without a row map it is the block's first pre-activation, LN(x) with the norm1 affine then SiLU (src/sdec.cu:72-73).
 // Lanes per row: C/8 (8 channels per lane, one 16-byte load) up to 64, so a 64-channel row is 8 lanes and a
 // wavefront handles 8 rows; the row sums reduce with lane shuffles inside the row's lane group.
+#include "lnact.h"
 #include "spconv.h"
 
 namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kOOR = 0xffff0000u;
 
-__device__ __forceinline__ float h2f(uint16_t h, bool bf) {
-  return bf ? __uint_as_float((uint32_t)h << 16) : (float)__builtin_bit_cast(_Float16, h);
-}
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack2(float lo, float hi, bool bf) {
-  return bf ? __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2))
-            : __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
-}
+__device__ __forceinline__ float h2f(uint16_t h, bool bf) { return lnact_h2f(h, bf); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, bool bf) { return lnact_pack2(lo, hi, bf); }
 
 // LPR lanes per row, CH = C / (8 * LPR) 16-byte chunks per lane
 template <int LPR, int CH>
@@ -37,44 +30,21 @@ __global__ void __launch_bounds__(256) k_gather_ln_act(const uint16_t* __restric
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, (int)x_bytes,
                                                                       0x00020000);
   float v[CH][8];
-  float s = 0.f;
 #pragma unroll
   for (int k = 0; k < CH; k++) {
     const int c8 = (k * LPR + sub) * 8;
     const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (r * (uint32_t)C + c8) * 2u : kOOR, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      v[k][j] = h2f((uint16_t)(q[j >> 1] >> ((j & 1) * 16)), bf);
-      s += v[k][j];
-    }
+    for (int j = 0; j < 8; j++) v[k][j] = h2f((uint16_t)(q[j >> 1] >> ((j & 1) * 16)), bf);
   }
-#pragma unroll
-  for (int d = 1; d < LPR; d <<= 1) s += __shfl_xor(s, d, 64);
-  const float mean = s / (float)C;
-  float q2 = 0.f;
-#pragma unroll
-  for (int k = 0; k < CH; k++)
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const float d = v[k][j] - mean;
-      q2 += d * d;
-    }
-#pragma unroll
-  for (int d = 1; d < LPR; d <<= 1) q2 += __shfl_xor(q2, d, 64);
-  const float rstd = rsqrtf(q2 / (float)C + eps);
+  float mean, rstd;
+  ln_stats<LPR, CH>(v, C, eps, mean, rstd);
   if (!live) return;
 #pragma unroll
   for (int k = 0; k < CH; k++) {
     const int c8 = (k * LPR + sub) * 8;
     float o[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      float t = (v[k][j] - mean) * rstd;
-      if (gamma) t *= gamma[c8 + j];
-      if (beta) t += beta[c8 + j];
-      if (silu) t = t * __builtin_amdgcn_rcpf(1.0f + __expf(-t));
-      o[j] = t;
-    }
+    ln_out8(v[k], mean, rstd, gamma ? gamma + c8 : nullptr, beta ? beta + c8 : nullptr, silu, o);
     *(u32x4*)&y[i * C + c8] = u32x4{pack2(o[0], o[1], bf), pack2(o[2], o[3], bf), pack2(o[4], o[5], bf),
                                     pack2(o[6], o[7], bf)};
   }

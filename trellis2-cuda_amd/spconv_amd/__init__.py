@@ -30,7 +30,7 @@ SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build
            "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
            "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subm_conv_skip",
            "spc_subdivide", "spc_subdivide_noalloc", "spc_subm_conv_replay", "spc_grid_sample_map",
-           "spc_grid_sample_sum", "spc_subdivide_build")
+           "spc_grid_sample_sum", "spc_subdivide_build", "spc_subm_conv_preln")
 
 _lib = None
 
@@ -71,6 +71,8 @@ def load_library():
     L.spc_grid_sample_map.argtypes = [P, P, I64, I, I, P, P]
     L.spc_grid_sample_sum.argtypes = [P, I64, I, P, P, I64, P]
     L.spc_subdivide_build.argtypes = [P, P, I64, I, I, I, P, P, ctypes.POINTER(I64), PP]
+    L.spc_subm_conv_preln.argtypes = [P, I64, P, I, P, P, ctypes.c_float, I, P, P, I, I, I, P, I64, I, P, I64, I, I,
+                                      P, P]
     for name in SYMBOLS:
         if name != "spc_last_error":
             getattr(L, name).restype = I
@@ -338,6 +340,37 @@ def subm_conv_skip(x, w, b, cache: SpConvCache, x_skip, src, act: int = ACT_NONE
         out = torch.empty((N, Co), dtype=x.dtype, device=x.device)
     _check(load_library().spc_subm_conv_skip(_ptr(x), _ptr(w), _ptr(b), _dt(x), _dt(b) if b is not None else F32, act,
                                              _ptr(x_skip), n_skip, Cin, _ptr(src), N, Ci, Co, cache._h, _ptr(out)))
+    return out
+
+
+def subm_conv_preln(x_src, w, b, cache: SpConvCache, row_map=None, shift: int = 0, gamma=None, beta=None,
+                    eps: float = 1e-6, pre_act: int = ACT_SILU, act: int = ACT_NONE, x_skip=None, skip_src=None,
+                    out=None):
+    """act(subm_conv3d(pre_act(LayerNorm(x_src[row_map >> shift]) * gamma + beta), w) + b) [+ the skip of
+    subm_conv_skip when x_skip / skip_src are given]: the upsample block's norm2 + SiLU + conv2 + skip
+    (src/sdec.cu:78-84). gather_ln_act then the conv; with SPCONV_PRELN_FUSED=1 in the environment, one kernel for
+    64 -> 64 convs whose halo schedule has no spill tiles; the same bits either way. out has x_src's 16-bit
+    dtype."""
+    torch = _torch()
+    M, Ci = x_src.shape
+    Co = w.shape[0]
+    N = cache.N
+    if row_map is not None and (row_map.dtype != torch.int32 or row_map.numel() != N):
+        raise ValueError(f"row_map must be int32 [{N}]")
+    for name, t in (("gamma", gamma), ("beta", beta)):
+        if t is not None and (t.dtype != torch.float32 or t.numel() != Ci):
+            raise ValueError(f"{name} must be float32 [{Ci}]")
+    if (x_skip is None) != (skip_src is None):
+        raise ValueError("x_skip and skip_src go together")
+    if skip_src is not None and (skip_src.dtype != torch.int32 or skip_src.numel() != N):
+        raise ValueError(f"skip_src must be int32 [{N}]")
+    n_skip, Cin = x_skip.shape if x_skip is not None else (0, 0)
+    if out is None:
+        out = torch.empty((N, Co), dtype=x_src.dtype, device=x_src.device)
+    _check(load_library().spc_subm_conv_preln(
+        _ptr(x_src), M, _ptr(row_map), shift, _ptr(gamma), _ptr(beta), eps, pre_act, _ptr(w), _ptr(b), _dt(x_src),
+        _dt(b) if b is not None else F32, act, _ptr(x_skip), n_skip, Cin, _ptr(skip_src), N, Ci, Co, cache._h,
+        _ptr(out)))
     return out
 
 
