@@ -131,6 +131,10 @@ struct ConvArgs {
   // xs of them run whole, each later one is split into xk[x] workgroups over its K stages, which write fp32
   // partial tiles [BM][256] from slot xpart0[x] on; k_split_reduce sums them and applies the epilogue.
   float* part;
+  // tail-split schedule (part set): logical tiles numbered channel-tile-major (tile = tn * tiles_m + tm), so the
+  // contiguous range an XCD walks stays on one 256-column weight slice instead of cycling through all of them
+  // (C2, 768 -> 768: 32 MB of weights, past L2; 0.298 -> 0.287 ms)
+  int tnmaj;
   int xt0[9], xk[8], xpart0[8], xs;
 };
 
@@ -1288,8 +1292,9 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
     logical = (g % 8) * per + g / 8;
   }
   if (logical >= a.tiles_m * a.tiles_n) return;
-  const int tm_ = a.tsched && !a.part ? a.tsched[logical / a.tiles_n] : logical / a.tiles_n;
-  const int tn_ = logical % a.tiles_n;
+  const bool tmaj = a.tnmaj;  // set only with the tail-split schedule (no tsched)
+  const int tm_ = a.tsched && !a.part ? a.tsched[logical / a.tiles_n] : tmaj ? logical % a.tiles_m : logical / a.tiles_n;
+  const int tn_ = tmaj ? logical / a.tiles_m : logical % a.tiles_n;
   const int row0 = tm_ * BM, co0 = tn_ * (64 * NW);
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), wn = wv;
@@ -1856,7 +1861,8 @@ __global__ void __launch_bounds__(256) k_split_reduce(ConvArgs a) {
   }
   if (x == 8) return;
   const int kx = a.xk[x], logical = a.xt0[x] + a.xs + st, pbase = a.xpart0[x] + st * kx;
-  const int tm_ = logical / a.tiles_n, tn_ = logical % a.tiles_n;
+  const int tm_ = a.tnmaj ? logical % a.tiles_m : logical / a.tiles_n;
+  const int tn_ = a.tnmaj ? logical / a.tiles_m : logical % a.tiles_n;
   const int row = tm_ * BM + r, col = tn_ * 256 + c8;
   float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < kx; j++) {
@@ -1948,6 +1954,7 @@ void launch_wide_dma(ConvArgs a) {
     }
   }
   if (a.part) a.tsched = nullptr;  // the tail split keeps the XCD-contiguous walk
+  a.tnmaj = a.part != nullptr;
   k_conv_wide_dma<F16, BM><<<a.grid, 256, 0, stream()>>>(a);
   if (a.part) {
     int ntail = 0;
