@@ -37,6 +37,9 @@ def test_error_convention_without_gpu():
     assert b"null" in lib.spc_last_error()
     assert lib.spc_subm_conv(None, None, None, 2, 0, 4, 32, 64, None, None) == -1
     assert b"cache is null" in lib.spc_last_error()
+    assert lib.spc_subm_conv_preln(None, 0, None, 0, None, None, 1e-6, 1, None, None, 2, 0, 0, None, 0, 0, None, 4,
+                                   64, 64, None, None) == -1
+    assert b"cache is null" in lib.spc_last_error()
     b1, bk, s = spconv_amd.spconv_cfg(400000, 256, 256)
     assert (b1, bk, s) == (128, 64, 1)
     assert spconv_amd.spconv_cfg(1000, 32, 64)[1] == 32
