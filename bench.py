@@ -197,6 +197,28 @@ def measure(name, args, torch, np, sp, W, cpu, want_cpu, cpu_seconds, extras):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # settle: the clock under a sustained conv load falls for the first few hundred ms (power management), so keep
+    # launching in batches until at least --settle seconds have passed and a batch is no faster than the one before;
+    # the timed steps then run at the clock a long run sees (and that a profiler run of the same command averages)
+    settle = {"batches": 0, "seconds": 0.0, "batch_ms": []}
+    t_settle = time.perf_counter()
+    prev = None
+    while True:
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record(stream)
+        for _ in range(20):
+            step()
+        eb.record(stream)
+        torch.cuda.synchronize()
+        cur = ea.elapsed_time(eb) / 20
+        settle["batches"] += 1
+        settle["batch_ms"].append(round(cur, 4))
+        el = time.perf_counter() - t_settle
+        if (el >= args.settle and prev is not None and cur >= 0.995 * prev) or el >= 5 * max(args.settle, 0.2):
+            break
+        prev = cur
+    settle["seconds"] = round(time.perf_counter() - t_settle, 3)
+    settle["batch_ms"] = settle["batch_ms"][:3] + settle["batch_ms"][-3:]
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t_wall = time.perf_counter()
     e0.record(stream)
@@ -206,20 +228,36 @@ def measure(name, args, torch, np, sp, W, cpu, want_cpu, cpu_seconds, extras):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
     ms = e0.elapsed_time(e1) / args.steps
+    # the conv kernels alone (HIP events the library records on its stream around each call's conv kernels: the
+    # per-call weight repack falls outside), the same number of steps right after
+    sp.kernel_timing(True)
+    for _ in range(args.steps):
+        step()
+    sp.kernel_timing(False)
+    kts = sp.kernel_times()
+    kernel_ms = float(np.mean(kts)) if kts else ms
 
     flops = 2.0 * P * ci * co
     tflops = flops / (ms * 1e-3) / 1e12
+    k_tflops = flops / (kernel_ms * 1e-3) / 1e12
     comp_bytes = n * ci * 2 + n * 27 * 4 + 27 * ci * co * 2 + co * 4 + (n * co * 2 if res is not None else 0) \
         + n * co * 2 + n * 4
     gbs = comp_bytes / (ms * 1e-3) / 1e9
+    k_gbs = comp_bytes / (kernel_ms * 1e-3) / 1e9
     wide = ci >= 256 or co >= 256
     traffic, tdig = traffic_for(cfg.name, args.digest)
+    # achieved / frac: per conv-kernel launch (algorithmic work / the kernels' event-timed duration); the *_step
+    # figures divide by the whole step (weight repack included) instead
     if wide:
-        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
+        roof = {"bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(k_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                "achieved_step": round(tflops, 2), "frac_step": round(tflops / PEAK_BF16_TFLOPS, 4)}
     else:
-        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic}
+        roof = {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                "achieved_step": round(gbs, 1), "frac_step": round(gbs / PEAK_HBM_GBS, 4)}
+    roof["kernel_ms"] = round(kernel_ms, 5)
+    roof["step_ms"] = round(ms, 5)
     roof["algorithmic_flops"] = flops
     roof["compulsory_bytes"] = comp_bytes
     if traffic is not None:
@@ -229,6 +267,7 @@ def measure(name, args, torch, np, sp, W, cpu, want_cpu, cpu_seconds, extras):
 
     out = {"workload": f"{cfg.name}: {cfg.grid}^3 shell N={n} Ci={ci} Co={co} bf16 {cfg.epilogue}",
            "N": n, "Ci": ci, "Co": co, "active_pairs": P, "ms_per_step": round(ms, 5),
+           "kernel_ms": round(kernel_ms, 5), "settle": settle,
            "tflops": round(tflops, 3), "mvox_per_s": round(n / (ms * 1e-3) / 1e6, 2), "compulsory_GBps": round(gbs, 1),
            "roofline": roof, "kmap_build": kmap, "first_call": first,
            "executed_over_active_pairs": round(executed_pairs / max(P, 1), 4), "skip_group_rows": gsz,
@@ -298,9 +337,15 @@ def measure(name, args, torch, np, sp, W, cpu, want_cpu, cpu_seconds, extras):
         def torch_preact():
             torch.nn.functional.silu(torch.nn.functional.layer_norm(h1[src.long()].float(), (co2,), eps=1e-6)).to(
                 torch.bfloat16)
+        prev_env = os.environ.get("SPCONV_PRELN_FUSED")
         os.environ["SPCONV_PRELN_FUSED"] = "1"  # the one-kernel form is opt-in (read per call)
-        one_kernel_ms = round(timed(half_one_kernel, 10), 4)
-        del os.environ["SPCONV_PRELN_FUSED"]
+        try:
+            one_kernel_ms = round(timed(half_one_kernel, 10), 4)
+        finally:
+            if prev_env is None:
+                os.environ.pop("SPCONV_PRELN_FUSED", None)
+            else:
+                os.environ["SPCONV_PRELN_FUSED"] = prev_env
         e2e["second_half"] = {
             "children": len(ch), "Co": co2,
             "gather_ln_silu_then_conv_ms": round(timed(half_gathered_rows, 10), 4),
@@ -375,6 +420,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c3")
+    ap.add_argument("--settle", type=float, default=1.0,
+                    help="seconds of untimed launches after --warmup, until the per-launch time stops falling")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU work of the headline cpu_baseline")
     ap.add_argument("--cpu-seconds-extra", type=float, default=4.0, help="CPU work of each other config's baseline")
@@ -466,7 +513,8 @@ def main():
         "dtype": "bf16", "data": "synthetic (seeded union-of-shapes shell, random N(0,1) features, N(0,1/(27Ci)) "
                                  "weights)",
         "config": cfg,
-        "roofline": {k: r[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+        "roofline": {k: r[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel_ms", "step_ms",
+                                       "achieved_step", "frac_step")},
         "cpu_baseline": head.get("cpu_baseline"),
         "extras": dict(keep, roofline_detail=r, measured_peaks=measured, configs=others, source_digest=args.digest,
                        host_cpu=cpu),

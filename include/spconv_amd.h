@@ -98,6 +98,13 @@ int spc_conv_cfg(int64_t N, int Ci, int Co, int* B1, int* BK, int* S);
  * Replaces: spconv_cfg's table replay (src/spconv.cu:176-221). */
 int spc_conv_cfg_autotune(const char* path, const char* device, int64_t N, int Ci, int Co, int* B1, int* BK, int* S);
 
+/* spc_conv_cfg_autotune with strict replay: when `strict` is nonzero (or the environment has T2_STRICT=1, which
+ * spc_conv_cfg_autotune honours too) a (N, Ci, Co) the file has no tile entry for is an error (-1 and
+ * spc_last_error) instead of the 128/64 default, so a replayed tile cannot be mistaken for a default one.
+ * Replaces: spconv_cfg's strict mode (src/spconv.cu:219). */
+int spc_conv_cfg_autotune_strict(const char* path, const char* device, int64_t N, int Ci, int Co, int strict, int* B1,
+                                 int* BK, int* S);
+
 /* out[N,Co] (dtype = x's) = subm_conv3d(x [N,Ci], w [Co,27,Ci], b [Co] or NULL).
  * x and w: both SPC_F16 or both SPC_BF16; b_dtype: SPC_F32/F16/BF16. Ci % 32 == 0, Co % 64 == 0.
  * Replaces: subm_conv (src/spconv.h:15-16, src/spconv.cu:159-175); the output buffer is the caller's. */
@@ -202,6 +209,19 @@ int spc_subdivide_build(const int32_t* coords, const uint16_t* logits_f16, int64
  * cannot allocate device memory or block on the host (code under HIP graph capture, tight serving loops). Its
  * scratch (per-parent counts and scan sums, about 16 MiB) is a static device array that each GPU holds until the
  * process ends, so n <= 4194304 (larger n fails with an error) and calls that overlap on one GPU race. */
+/* Conv-kernel timing. spc_kernel_timing(1) clears the list and starts bracketing each conv call's conv kernels (split-K
+ * reduction and spill-tile kernel included; weight repack and first-call schedules excluded) with HIP events on the
+ * library stream; spc_kernel_timing(0) stops. spc_kernel_times waits for the recorded events and writes up to `max`
+ * per-call kernel times (ms, call order) to ms, their number to *n. No counterpart in the reference (its parity app
+ * times whole calls, apps/parity.cu:148-167): it separates the kernels from the per-call weight repack. */
+int spc_kernel_timing(int on);
+int spc_kernel_times(float* ms, int max, int* n);
+
+/* Device allocations the library has made in this process: *requests counts every nonzero-sized allocation request
+ * (served from its free lists or not), *driver_allocs the hipMallocAsync calls among them. No counterpart in the
+ * reference: a diagnostic for callers that must not allocate (compare the counts around a call). Host only. */
+int spc_alloc_counts(int64_t* requests, int64_t* driver_allocs);
+
 int spc_subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
                           int32_t* src, int64_t* m_dev);
 

@@ -64,3 +64,19 @@ def test_unknown_device_and_missing_file():
     assert sp.spconv_cfg_autotune(FIX, "AMD Instinct MI355X", 1 << 18, 128, 128) == (128, 64, 1)
     with pytest.raises(RuntimeError):
         sp.spconv_cfg_autotune(FIX + ".missing", DEV, 100, 64, 64)
+
+
+def test_strict_replay(monkeypatch):
+    """Strict replay (src/spconv.cu:219): a hit returns the replayed tile, a miss is an error instead of the default,
+    by argument or by T2_STRICT=1 in the environment (which the plain entry point honours too)."""
+    assert sp.spconv_cfg_autotune(FIX, DEV, 1 << 18, 128, 128, strict=True) == (64, 32, 1)
+    with pytest.raises(RuntimeError, match="no autotune entry"):
+        sp.spconv_cfg_autotune(FIX, DEV, 1000, 48, 48, strict=True)
+    with pytest.raises(RuntimeError, match="no autotune entry"):
+        sp.spconv_cfg_autotune(FIX, "AMD Instinct MI355X", 1 << 18, 128, 128, strict=True)
+    assert sp.spconv_cfg_autotune(FIX, DEV, 1000, 48, 48) == (128, 64, 1)
+    monkeypatch.setenv("T2_STRICT", "1")
+    with pytest.raises(RuntimeError, match="no autotune entry"):
+        sp.spconv_cfg_autotune(FIX, DEV, 1000, 48, 48)
+    monkeypatch.setenv("T2_STRICT", "0")
+    assert sp.spconv_cfg_autotune(FIX, DEV, 1000, 48, 48) == (128, 64, 1)

@@ -347,6 +347,20 @@ def test_replay_split_k(gpu, ci, co, cfg):
     assert bad.float().mean() <= 5e-3
 
 
+def test_replay_empty_null_buffers(gpu):
+    """spc_subm_conv_replay on an empty cache accepts null buffers like its sibling entry points (N == 0: nothing is
+    read or written); a nonempty call with a null buffer is an error."""
+    import ctypes
+    lib = sp.load_library()
+    cache = sp.build_neighbors(torch.zeros((0, 4), dtype=torch.int32, device=gpu))
+    assert lib.spc_subm_conv_replay(None, None, None, None, 0, 0, 64, 64, 128, 64, 1, cache._h, None) == 0, \
+        lib.spc_last_error()
+    c = shell(3.0)
+    full = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    assert lib.spc_subm_conv_replay(None, None, None, None, 0, len(c), 64, 64, 128, 64, 1, full._h, None) == -1
+    assert b"null argument" in lib.spc_last_error()
+
+
 def test_replay_split_order_known_answer(gpu):
     """One isolated voxel, Ci = 256, BK = 32, S = 8: split s holds exactly the 32-channel chunk s of the centre offset.
     The weights make chunk s's partial p_s = (32768, 2^-9, 0, 0, -32768, 2^-9, 0, 0) for output channel 0, and the
@@ -567,3 +581,63 @@ def test_w256_widths(gpu, monkeypatch, ci, co):
     c = shell(10.0)
     run_case(gpu, c, ci, co, act=1, res_dt="bf16", seed=3)
     run_case(gpu, c, ci, co, in_dt="f16", out_dt="f16", act=0, res_dt="f32", seed=4)
+
+
+def test_c5_gathered_full(gpu):
+    """The timed cascade upsample path at C5's full size: subdivide_build on the 0.8 M parents, then
+    subm_conv_gathered(x_parents, src, 3) 128 -> 64 with bias + SiLU on the fresh children's cache; every child row
+    against the fp32 oracle on the gathered rows x_parents[src >> 3] (reference k_gather_rows + subm_conv,
+    src/sdec.cu:34-43,70-87), fp32 and bf16 outputs."""
+    cfg = W.CONFIGS["c5"]
+    par = W.shell_coords(cfg)
+    lg = W.keep_logits(len(par), cfg.keep_frac, cfg.seed)
+    ch, src, cc = sp.subdivide_build(torch.from_numpy(par).to(gpu),
+                                     torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16))
+    n = len(ch)
+    print(f"c5 gathered full: parents={len(par)} children={n}", flush=True)
+    w, b = W.conv_params(cfg)
+    tx, qx = quantize(W.features(len(par), cfg.ci, 21), "bf16")
+    tw, qw = quantize(w, "bf16")
+    xs, ws, bs = tx.to(gpu), tw.to(gpu), torch.from_numpy(b).to(gpu)
+    y32 = sp.subm_conv_gathered(xs, src, 3, ws, bs, cc, act=1, out_dtype=torch.float32)
+    y16 = sp.subm_conv_gathered(xs, src, 3, ws, bs, cc, act=1)
+    assert torch.equal(y16, y32.to(torch.bfloat16)), "bf16 output is not round(fp32 output)"
+    xg = qx[src.long().cpu().numpy() >> 3]
+    nbr, _, _, _ = oracle.build_neighbors(ch.cpu().numpy())
+    ref = oracle.conv(xg, qw, b, nbr, act=1)
+    compare(y32, ref, "f32", "c5 gathered fp32")
+    compare(y16, ref, "bf16", "c5 gathered bf16")
+
+
+def test_c5_conv_skip_full(gpu):
+    """subm_conv_skip (conv2 64 -> 64 + bias + SiLU with the c2s skip fused into the epilogue) on C5's children at
+    full size: every row against the fp32 oracle with the skip rows repeat_interleave(C2S(x_parents)) as its
+    residual (reference conv2 + k_add_skip, src/sdec.cu:38-43,82-84). The fused form rounds once; conv + add_skip
+    rounds twice, so the two are compared to the oracle separately."""
+    cfg = W.CONFIGS["c5"]
+    par = W.shell_coords(cfg)
+    lg = W.keep_logits(len(par), cfg.keep_frac, cfg.seed)
+    ch, src, cc = sp.subdivide_build(torch.from_numpy(par).to(gpu),
+                                     torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16))
+    n, cin, co = len(ch), cfg.ci, 64
+    print(f"c5 conv skip full: children={n}", flush=True)
+    w, b = W.conv_params(W.Config("t", 0, 0, (0, 0), False, 0, co, co, "bf16", "", 61))
+    th, qh = quantize(W.features(n, co, 22), "bf16")
+    tp, qp = quantize(W.features(len(par), cin, 23), "bf16")
+    tw, qw = quantize(w, "bf16")
+    h, xp, ws, bs = th.to(gpu), tp.to(gpu), tw.to(gpu), torch.from_numpy(b).to(gpu)
+    y = sp.subm_conv_skip(h, ws, bs, cc, xp, src, act=1)
+    y2 = sp.subm_conv_fused(h, ws, bs, cc, act=1)
+    sp.add_skip(y2, xp, src)
+    s = src.long().cpu().numpy()
+    rep = co // (cin // 8)
+    cols = (s[:, None] & 7) * (cin // 8) + np.arange(co)[None, :] // rep
+    skip = qp[(s >> 3)[:, None], cols]
+    nbr, _, _, _ = oracle.build_neighbors(ch.cpu().numpy())
+    ref = oracle.conv(qh, qw, b, nbr, res=skip, act=1)
+    compare(y, ref, "bf16", "c5 conv skip (fused)")
+    yr, y2r = y.float().cpu().numpy(), y2.float().cpu().numpy()
+    rel2 = np.linalg.norm(y2r - ref) / np.linalg.norm(ref)
+    assert rel2 <= 2e-3 and np.all(np.abs(y2r - ref) <= np.maximum(2e-2, 2 * ulp(ref, "bf16"))), \
+        f"conv + add_skip: rel-L2 {rel2:.3g}"
+    assert np.linalg.norm(yr - ref) <= np.linalg.norm(y2r - ref) * 1.01, "one rounding should not be worse than two"

@@ -40,7 +40,10 @@ def test_subdivide_noalloc_matches(gpu):
         print(f"subdivide_noalloc case {name} n={len(par)}", flush=True)
         tp = torch.from_numpy(par).to(gpu)
         tl = torch.from_numpy(lg.view(np.int16)).to(gpu).view(torch.float16)
+        torch.cuda.synchronize()
+        before = sp.alloc_counts()
         nc, ns = _noalloc(lib, tp, tl)
+        assert sp.alloc_counts() == before, "spc_subdivide_noalloc requested device memory from the library"
         rc, rs = sp.subdivide(tp, tl)
         assert nc.shape == rc.shape and ns.shape == rs.shape
         assert torch.equal(nc, rc) and torch.equal(ns, rs)
@@ -51,6 +54,7 @@ def test_subdivide_noalloc_matches(gpu):
 
 def test_subdivide_noalloc_empty_and_limit(gpu):
     lib = sp.load_library()
+    sp.set_stream(torch.cuda.current_stream())
     m = torch.full((1,), -1, dtype=torch.int64, device=gpu)
     assert lib.spc_subdivide_noalloc(None, None, 0, None, None, ctypes.c_void_p(m.data_ptr())) == 0
     assert int(m.item()) == 0

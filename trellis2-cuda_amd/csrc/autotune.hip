@@ -11,6 +11,7 @@
 //   <M>_splitk.<...>_splitk_kernel        "(L, Ci, Co, 27, S, True, ...)"     -> {"kwargs": {"B1", "BK", ...}}
 //   <M>.<...>_kernel                      "(L, Ci, Co, 27, True, ...)"        -> same, S = 1 (read last, so it wins)
 // with L = floor(log2 N). Missing entries give B1 = 128, BK = 64, S = 1, the reference's fallback.
+#include <cstdlib>
 #include <fstream>
 #include <map>
 #include <sstream>
@@ -189,7 +190,7 @@ Table load_table(const std::string& path, const std::string& device) {
 }
 }  // namespace
 
-SpConvCfg spconv_cfg_autotune(const std::string& path, const std::string& device, i64 N, int Ci, int Co) {
+SpConvCfg spconv_cfg_autotune(const std::string& path, const std::string& device, i64 N, int Ci, int Co, bool strict) {
   static std::map<std::pair<std::string, std::string>, Table> cache;  // callers serialize (the C ABI holds a mutex)
   auto it = cache.find({path, device});
   if (it == cache.end()) it = cache.emplace(std::make_pair(path, device), load_table(path, device)).first;
@@ -203,6 +204,11 @@ SpConvCfg spconv_cfg_autotune(const std::string& path, const std::string& device
   if (ti != t.tiles.end()) {
     c.B1 = ti->second.first;
     c.BK = ti->second.second;
+  } else {
+    // strict replay: a miss is an error instead of the (128, 64, S) default, as the reference does under
+    // T2_STRICT=1 (src/spconv.cu:219), so a replayed tile is never mistaken for a default one
+    const char* e = getenv("T2_STRICT");
+    REQ(!(strict || (e && std::string(e) == "1")), "no autotune entry for N=2^%d Ci=%d Co=%d S=%d", L, Ci, Co, S);
   }
   return c;
 }

@@ -1,5 +1,6 @@
 // extern "C" boundary over the C++ API, with the reference's embedding convention (apps/t2lib.cu:1-23):
 // 0 / -1 + last error string, all calls serialized by one mutex, exceptions never cross the ABI.
+#include <algorithm>
 #include <exception>
 #include <mutex>
 
@@ -256,16 +257,21 @@ SPC_API int spc_add_skip(void* h, const void* x, const int32_t* src, int64_t m, 
   });
 }
 
-SPC_API int spc_conv_cfg_autotune(const char* path, const char* device, int64_t N, int Ci, int Co, int* B1, int* BK,
-                                  int* S) {
+SPC_API int spc_conv_cfg_autotune_strict(const char* path, const char* device, int64_t N, int Ci, int Co, int strict,
+                                         int* B1, int* BK, int* S) {
   return guarded([&] {
     REQ(path && device && B1 && BK && S, "null argument");
     REQ(N >= 0 && Ci > 0 && Co > 0, "N=%lld Ci=%d Co=%d", (long long)N, Ci, Co);
-    const SpConvCfg c = spconv_cfg_autotune(path, device, N, Ci, Co);
+    const SpConvCfg c = spconv_cfg_autotune(path, device, N, Ci, Co, strict != 0);
     *B1 = c.B1;
     *BK = c.BK;
     *S = c.S;
   });
+}
+
+SPC_API int spc_conv_cfg_autotune(const char* path, const char* device, int64_t N, int Ci, int Co, int* B1, int* BK,
+                                  int* S) {
+  return spc_conv_cfg_autotune_strict(path, device, N, Ci, Co, 0, B1, BK, S);
 }
 
 SPC_API int spc_subm_conv(const void* x, const void* w, const void* b, int dtype, int b_dtype, int64_t N, int Ci,
@@ -273,10 +279,35 @@ SPC_API int spc_subm_conv(const void* x, const void* w, const void* b, int dtype
   return spc_subm_conv_fused(x, w, b, nullptr, dtype, b_dtype, SPC_F32, dtype, SPC_ACT_NONE, N, Ci, Co, c, out);
 }
 
+SPC_API int spc_kernel_timing(int on) {
+  return guarded([&] { kernel_timing(on != 0); });
+}
+
+SPC_API int spc_kernel_times(float* ms, int max, int* n) {
+  return guarded([&] {
+    REQ(n && (max <= 0 || ms), "null argument");
+    const std::vector<float> t = kernel_times();
+    const int k = (int)std::min<size_t>(t.size(), (size_t)std::max(max, 0));
+    for (int i = 0; i < k; i++) ms[i] = t[i];
+    *n = (int)t.size();
+  });
+}
+
+SPC_API int spc_alloc_counts(int64_t* requests, int64_t* driver_allocs) {
+  return guarded([&] {
+    REQ(requests && driver_allocs, "null argument");
+    i64 r = 0, d = 0;
+    alloc_counts(&r, &d);
+    *requests = r;
+    *driver_allocs = d;
+  });
+}
+
 SPC_API int spc_subm_conv_replay(const void* x, const void* w, const void* b, const void* residual, int act, int64_t N,
                                  int Ci, int Co, int B1, int BK, int S, spc_cache* c, void* out) {
   return guarded([&] {
-    REQ(c && x && w && out, "null argument");
+    REQ(c, "cache is null");
+    REQ(N == 0 || (x && w && out), "null argument");  // empty input: argument checks only, null buffers allowed
     Tensor tx = borrow(x, {N, Ci}, F16), tw = borrow(w, {Co, 27, Ci}, F16), to = borrow(out, {N, Co}, F16);
     Tensor tb, tr;
     if (b) tb = borrow(b, {Co}, F16);

@@ -2103,6 +2103,30 @@ __global__ void k_gather_rows(const u32x4* __restrict__ x, i64 m, int units, con
   out[q] = r < (uint64_t)m ? x[(i64)r * units + (q - i * units)] : u32x4{0, 0, 0, 0};
 }
 
+// Conv-kernel timer (off unless kernel_timing(true)): while on, every conv call records a HIP event on the library
+// stream right before its first conv kernel and right after its last (split-K reduction and spill-tile kernel
+// included; weight repack, bias conversion and first-call schedules excluded), so a caller can time the kernels
+// alone. Events are pooled and reused after kernel_timing(true) resets the list.
+struct KernelTimer {
+  bool on = false;
+  std::vector<hipEvent_t> ev;
+  size_t used = 0;
+};
+KernelTimer& ktimer() {
+  static KernelTimer t;
+  return t;
+}
+void ktimer_mark() {
+  KernelTimer& t = ktimer();
+  if (!t.on) return;
+  if (t.used == t.ev.size()) {
+    hipEvent_t e;
+    CK(hipEventCreate(&e));
+    t.ev.push_back(e);
+  }
+  CK(hipEventRecord(t.ev[t.used++], stream()));
+}
+
 // A second stream per device (default priority, like the library stream) with a fork and a join event, for the
 // spill tiles' gathering kernel, which runs beside the halo kernel. Created on first use, kept until the process ends.
 struct SideStream {
@@ -2319,6 +2343,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       map_table_rows(ht->spill.tbl, *row_map, shift, M, mtbl);
       sa.tbl = mtbl.ptr<uint32_t>();
     }
+    ktimer_mark();
     SideStream& ss = side_stream();
     CK(hipEventRecord(ss.fork, stream()));
     CK(hipStreamWaitEvent(ss.s, ss.fork, 0));
@@ -2330,11 +2355,14 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     else dispatch<false>(cfg, a);
     CK(hipGetLastError());
     CK(hipStreamWaitEvent(stream(), ss.join, 0));
+    ktimer_mark();
     return;
   }
+  ktimer_mark();
   if (x.dt == F16) dispatch<true>(cfg, a);
   else dispatch<false>(cfg, a);
   CK(hipGetLastError());
+  ktimer_mark();
 }
 
 void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, const Tensor& x_skip,
@@ -2451,4 +2479,22 @@ Tensor subm_conv(const Tensor& x, const Tensor& w, const Tensor* b, SpConvCache&
   Tensor y = empty({x.size(0), w.size(0)}, x.dt);
   subm_conv_fused(x, w, b, nullptr, ACT_NONE, c, y);
   return y;
+}
+
+void kernel_timing(bool on) {
+  KernelTimer& t = ktimer();
+  t.on = on;
+  if (on) t.used = 0;
+}
+
+std::vector<float> kernel_times() {
+  KernelTimer& t = ktimer();
+  std::vector<float> ms;
+  for (size_t i = 0; i + 1 < t.used; i += 2) {
+    CK(hipEventSynchronize(t.ev[i + 1]));
+    float v = 0.f;
+    CK(hipEventElapsedTime(&v, t.ev[i], t.ev[i + 1]));
+    ms.push_back(v);
+  }
+  return ms;
 }

@@ -70,6 +70,9 @@ struct Tensor {
 Tensor borrow(const void* p, std::vector<i64> sh, DT dt);
 Tensor empty(std::vector<i64> sh, DT dt);
 Tensor zeros(std::vector<i64> sh, DT dt);
+// Device allocations the library has made since the process started: every request to empty() with a nonzero size
+// (served from the free lists or not), and the hipMallocAsync calls among them.
+void alloc_counts(i64* requests, i64* driver_allocs);
 Tensor from_host(const void* src, std::vector<i64> sh, DT dt);
 std::vector<char> to_host(const Tensor& t);
 template <class T>

@@ -1,5 +1,6 @@
 #include "core.h"
 
+#include <atomic>
 #include <cstdarg>
 #include <mutex>
 #include <stdexcept>
@@ -67,6 +68,7 @@ size_t size_class(size_t n) {
   const size_t g = 2u << 20;
   return (n + g - 1) / g * g;
 }
+std::atomic<i64> g_alloc_requests{0}, g_driver_allocs{0};
 void keep_pool_memory(int dev) {
   static bool done[64] = {};
   if (dev < 0 || dev >= 64 || done[dev]) return;
@@ -96,7 +98,11 @@ Tensor empty(std::vector<i64> sh, DT dt) {
         fl.pop_back();
       }
     }
-    if (!p) CK(hipMallocAsync(&p, key.size, key.stream));
+    g_alloc_requests++;
+    if (!p) {
+      CK(hipMallocAsync(&p, key.size, key.stream));
+      g_driver_allocs++;
+    }
     t.p = p;
     t.own = std::shared_ptr<void>(p, [key](void* q) {
       std::lock_guard<std::mutex> g(g_alloc_mu);
@@ -104,6 +110,10 @@ Tensor empty(std::vector<i64> sh, DT dt) {
     });
   }
   return t;
+}
+void alloc_counts(i64* requests, i64* driver_allocs) {
+  *requests = g_alloc_requests.load();
+  *driver_allocs = g_driver_allocs.load();
 }
 Tensor zeros(std::vector<i64> sh, DT dt) {
   auto t = empty(std::move(sh), dt);

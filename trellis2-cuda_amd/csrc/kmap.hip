@@ -390,6 +390,10 @@ SpConvCache build_neighbors_impl(const int4* coords, i64 n, const uint32_t* ndev
 }
 }  // namespace
 
+SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D) {
+  return build_neighbors(coords, W, H, D, false);
+}
+
 SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep_hash) {
   REQ(coords.dt == I32 && coords.dim() == 2 && coords.size(1) == 4, "coords must be int32 [N,4]");
   return build_neighbors_impl(coords.ptr<int4>(), coords.size(0), nullptr, W, H, D, keep_hash);

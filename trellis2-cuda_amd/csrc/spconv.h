@@ -2,6 +2,7 @@
 // call-compatible so the sparse decoders (reference src/sdec.cu:15-18, 55, 92) can call it unchanged.
 #pragma once
 #include <map>
+#include <vector>
 #include <utility>
 
 #include "core.h"
@@ -72,7 +73,10 @@ struct SpConvCache {
 };
 // coords int32 [N,4] (b,x,y,z); keep_hash keeps the brick hash in the cache (~32-128 B + 256 B per voxel) so that
 // lookup() can answer arbitrary coordinate queries.
-SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep_hash = false);
+// The four-argument form is the reference's exact signature (src/spconv.h:12), so an object compiled against the
+// reference header links against this library unchanged.
+SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D);
+SpConvCache build_neighbors(const Tensor& coords, int W, int H, int D, bool keep_hash);
 
 // Row of each query coordinate (b,x,y,z) in the cache's voxel set, -1 when absent or outside [0,W)x[0,H)x[0,D)
 // (b < 0 included). The cache must have been built with keep_hash. Reference: the voxel hash probes of
@@ -103,8 +107,16 @@ struct SpConvCfg {
 };
 SpConvCfg spconv_cfg(int N, int Ci, int Co);
 // The reference's tile choice for (N, Ci, Co) replayed from a FlexGEMM autotune cache file, section `device`
-// (src/spconv.cu:176-221); B1 = 128, BK = 64, S = 1 where the file has no entry.
-SpConvCfg spconv_cfg_autotune(const std::string& path, const std::string& device, i64 N, int Ci, int Co);
+// (src/spconv.cu:176-221); B1 = 128, BK = 64, S = 1 where the file has no entry, or an error when `strict` is set or
+// the environment has T2_STRICT=1 (src/spconv.cu:219).
+SpConvCfg spconv_cfg_autotune(const std::string& path, const std::string& device, i64 N, int Ci, int Co,
+                              bool strict = false);
+
+// Conv-kernel timing: while on, each conv call brackets its conv kernels (not the weight repack or first-call
+// schedules) with HIP events on the library stream; kernel_times() waits for them and returns each call's kernel ms
+// in call order. kernel_timing(true) clears the list. No counterpart in the reference (its apps time whole calls).
+void kernel_timing(bool on);
+std::vector<float> kernel_times();
 
 // y = subm_conv3d(x, w, b): x fp16/bf16 [N,Ci], w same dtype [Co,27,Ci], b fp16/bf16/fp32 [Co] or null.
 // Returns [N,Co] in x's dtype; fp32 accumulation, bias added to the fp32 sum before the single rounding.

@@ -27,10 +27,10 @@ EMPTY = 0xFFFFFFFF
 # the C ABI's exported symbols (every declaration of include/spconv_amd.h)
 SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build_neighbors_ex", "spc_cache_lookup",
            "spc_fdg_quads", "spc_cache_free", "spc_cache_info", "spc_cache_valid", "spc_conv_cfg",
-           "spc_conv_cfg_autotune", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
+           "spc_conv_cfg_autotune", "spc_conv_cfg_autotune_strict", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
            "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subm_conv_skip",
            "spc_subdivide", "spc_subdivide_noalloc", "spc_subm_conv_replay", "spc_grid_sample_map",
-           "spc_grid_sample_sum", "spc_subdivide_build", "spc_subm_conv_preln")
+           "spc_grid_sample_sum", "spc_subdivide_build", "spc_subm_conv_preln", "spc_alloc_counts", "spc_kernel_timing", "spc_kernel_times")
 
 _lib = None
 
@@ -58,6 +58,8 @@ def load_library():
     L.spc_conv_cfg.argtypes = [I64, I, I, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)]
     L.spc_conv_cfg_autotune.argtypes = [ctypes.c_char_p, ctypes.c_char_p, I64, I, I, ctypes.POINTER(I),
                                          ctypes.POINTER(I), ctypes.POINTER(I)]
+    L.spc_conv_cfg_autotune_strict.argtypes = [ctypes.c_char_p, ctypes.c_char_p, I64, I, I, I, ctypes.POINTER(I),
+                                                ctypes.POINTER(I), ctypes.POINTER(I)]
     L.spc_subm_conv.argtypes = [P, P, P, I, I, I64, I, I, P, P]
     L.spc_subm_conv_fused.argtypes = [P, P, P, P, I, I, I, I, I, I64, I, I, P, P]
     L.spc_subm_conv_gathered.argtypes = [P, I64, P, I, P, P, P, I, I, I, I, I, I64, I, I, P, P]
@@ -73,6 +75,9 @@ def load_library():
     L.spc_subdivide_build.argtypes = [P, P, I64, I, I, I, P, P, ctypes.POINTER(I64), PP]
     L.spc_subm_conv_preln.argtypes = [P, I64, P, I, P, P, ctypes.c_float, I, P, P, I, I, I, P, I64, I, P, I64, I, I,
                                       P, P]
+    L.spc_alloc_counts.argtypes = [ctypes.POINTER(I64), ctypes.POINTER(I64)]
+    L.spc_kernel_timing.argtypes = [I]
+    L.spc_kernel_times.argtypes = [ctypes.POINTER(ctypes.c_float), I, ctypes.POINTER(I)]
     for name in SYMBOLS:
         if name != "spc_last_error":
             getattr(L, name).restype = I
@@ -242,12 +247,13 @@ def spconv_cfg(N: int, Ci: int, Co: int):
     return b1.value, bk.value, s.value
 
 
-def spconv_cfg_autotune(path: str, device: str, N: int, Ci: int, Co: int):
+def spconv_cfg_autotune(path: str, device: str, N: int, Ci: int, Co: int, strict: bool = False):
     """(B1, BK, S) the reference would pick from a FlexGEMM autotune cache file for device section `device`
-    (reference spconv_cfg, src/spconv.cu:176-221); (128, 64, 1) where the file has no entry. Host only."""
+    (reference spconv_cfg, src/spconv.cu:176-221); (128, 64, 1) where the file has no entry, or RuntimeError when
+    `strict` (or T2_STRICT=1 in the environment, src/spconv.cu:219). Host only."""
     b1, bk, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    _check(load_library().spc_conv_cfg_autotune(os.fsencode(path), device.encode(), N, Ci, Co, ctypes.byref(b1),
-                                                ctypes.byref(bk), ctypes.byref(s)))
+    _check(load_library().spc_conv_cfg_autotune_strict(os.fsencode(path), device.encode(), N, Ci, Co, int(strict),
+                                                       ctypes.byref(b1), ctypes.byref(bk), ctypes.byref(s)))
     return b1.value, bk.value, s.value
 
 
@@ -423,6 +429,29 @@ def subdivide(coords, logits_f16):
     m = ctypes.c_int64()
     _check(load_library().spc_subdivide(_ptr(coords), _ptr(logits_f16), n, _ptr(cc), _ptr(src), ctypes.byref(m)))
     return cc[:m.value], src[:m.value]
+
+
+def kernel_timing(on: bool):
+    """Start (clearing earlier records) or stop bracketing each conv call's conv kernels with HIP events on the
+    library stream (the weight repack and first-call schedules fall outside)."""
+    _check(load_library().spc_kernel_timing(int(on)))
+
+
+def kernel_times():
+    """Per-call conv-kernel times (ms) recorded since kernel_timing(True), in call order (waits for them)."""
+    L = load_library()
+    n = ctypes.c_int()
+    _check(L.spc_kernel_times(None, 0, ctypes.byref(n)))
+    buf = (ctypes.c_float * max(n.value, 1))()
+    _check(L.spc_kernel_times(buf, n.value, ctypes.byref(n)))
+    return list(buf[:n.value])
+
+
+def alloc_counts():
+    """(allocation requests, hipMallocAsync calls) the library has made in this process (host only)."""
+    r, d = ctypes.c_int64(), ctypes.c_int64()
+    _check(load_library().spc_alloc_counts(ctypes.byref(r), ctypes.byref(d)))
+    return r.value, d.value
 
 
 def subdivide_build(coords, logits_f16, W: int = 4096, H: int = 4096, D: int = 4096):
