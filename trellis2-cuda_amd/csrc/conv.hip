@@ -110,6 +110,10 @@ struct ConvArgs {
   const uint16_t* hidx;
   const uint32_t* hgm;
   const int32_t* tsched;  // row tiles in dispatch order (SpConvCache::tile_schedule), for k_conv_w256
+  // spill tiles of the halo schedule (k_conv_narrow): workgroup g computes tile tlist[g] if g < *tcount, with the
+  // identity row order (tbl = nbr, gs = gray in input order) and exits otherwise
+  const int32_t* tlist;
+  const int32_t* tcount;
   const int32_t* rmap;  // gathered conv through the halo kernel: halo row h reads source row rmap[h] >> rshift
   int rshift, rmax;
   // skip residual (upsample block, halo kernel only): residual[i, c] = skip_x[src[i] >> 3, (src[i] & 7) * Cin/8 +
@@ -725,6 +729,31 @@ __device__ __forceinline__ uint32_t nbr_offset(uint32_t n, uint32_t rowbytes) {
   return n == EMPTY ? kOutOfRange : n * rowbytes;
 }
 
+// 8 consecutive channels c8.. of the skip residual of one output row, as 8 x 16-bit in r (src < 0 or past the
+// source rows: zeros). Channel c reads element c / rep of the parent's slot, so 8 channels need 8 / rep elements
+// (one for rep >= 8): one 16-, 8-, 4- or 2-byte load, widened by repeating each element rep times.
+__device__ __forceinline__ u32x4 load_skip8(const __amdgpu_buffer_rsrc_t& rs, const ConvArgs& a, int src, int c8,
+                                            bool ok) {
+  const uint32_t s = (uint32_t)src;
+  const bool live = ok && s < a.skip_n * 8u;
+  const uint32_t base = (s >> 3) * (uint32_t)a.skip_cin + (s & 7u) * (uint32_t)(a.skip_cin >> 3) +
+                        (uint32_t)(c8 / a.skip_rep);
+  const uint32_t off = live ? base * 2u : kOutOfRange;
+  auto dup = [](uint32_t v16) { return (v16 & 0xffffu) | (v16 << 16); };
+  if (a.skip_rep == 1) return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+  if (a.skip_rep == 2) {
+    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+    const u32x2v q = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    return u32x4{dup(q[0]), dup(q[0] >> 16), dup(q[1]), dup(q[1] >> 16)};
+  }
+  if (a.skip_rep == 4) {
+    const uint32_t q = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    return u32x4{dup(q), dup(q), dup(q >> 16), dup(q >> 16)};
+  }
+  const uint32_t q = dup(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+  return u32x4{q, q, q, q};
+}
+
 template <bool F16, int S, int T, int G>
 __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   constexpr int NT = 256, BM = 4 * 16 * G, CI = 32 * S, CO = 16 * T, WB = T * S * 64;  // WB: 16B units per offset
@@ -738,19 +767,25 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   __shared__ int vlist[32];
 
   const int g = blockIdx.x, per = a.grid / 8;
-  const int tile = (g % 8) * per + g / 8;
+  int tile = (g % 8) * per + g / 8;
+  if (a.tlist) {  // spill tiles of a halo schedule
+    if (g >= __builtin_amdgcn_readfirstlane(*a.tcount)) return;
+    tile = __builtin_amdgcn_readfirstlane(a.tlist[g]);
+  }
   if (tile >= a.tiles_m) return;
   const int row0 = tile * BM;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
   const int N = a.N;
 
   // prologue: the tile's block of the neighbour table goes to LDS by DMA; rows, 16-row masks from the same order
+  // (the table is padded to whole tiles, except nbr itself for spill tiles: rows past N read zeros there, which the
+  // zero mask of those rows keeps out of every result)
   dma_tile_table<BM, NT>(a, row0, srcT, tid);
   if (tid < BM) {
     const int row = row0 + tid;
     const bool live = row < N;
-    ordT[tid] = live ? a.order[row] : 0;
-    uint32_t gm = a.gs[row];  // padded rows have mask 0
+    ordT[tid] = live ? (a.order ? a.order[row] : row) : 0;
+    uint32_t gm = live ? a.gs[row] : 0u;
 #pragma unroll
     for (int d = 1; d < 16; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
     if ((tid & 15) == 0) gmask[tid >> 4] = gm;
@@ -838,7 +873,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   // latency hides behind the loop; no registers held). Rows past N read out of range and land as zeros.
   constexpr int RU = BM * CO * 2 / 16, RK = RU / NT;  // 16-byte units, DMA loads per lane
   static_assert(RK * NT == RU, "residual tile split");
-  const bool res16 = a.res && a.res_dt != F32;
+  const bool res16 = a.res && a.res_dt != F32 && !a.skip_src;  // (a skip residual is loaded in the epilogue)
   if (res16) {
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, a.res_bytes);
 #pragma unroll
@@ -891,7 +926,18 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   constexpr int NP = 16 / RPP;
   const Epi e = make_epi(a);
   u32x4 resv[G][NP][2];
-  if (a.res && !res16) {  // fp32 residual: straight to registers, all requested before the first group
+  if (a.skip_src) {  // skip residual of the upsample block (spill tiles of the fused conv + skip)
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.skip_x, a.skip_bytes);
+#pragma unroll
+    for (int i = 0; i < G; i++)
+#pragma unroll
+      for (int p = 0; p < NP; p++) {
+        const int lrow = wv * (16 * G) + i * 16 + p * RPP + lane / LPR;
+        const bool ok = row0 + lrow < N;
+        resv[i][p][0] = load_skip8(rs, a, ok ? a.skip_src[ordT[lrow]] : -1, c8, ok);
+        resv[i][p][1] = u32x4{0, 0, 0, 0};
+      }
+  } else if (a.res && !res16) {  // fp32 residual: straight to registers, all requested before the first group
 #pragma unroll
     for (int i = 0; i < G; i++)
 #pragma unroll
@@ -925,31 +971,6 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
   }
-}
-
-// 8 consecutive channels c8.. of the skip residual of one output row, as 8 x 16-bit in r (src < 0 or past the
-// source rows: zeros). Channel c reads element c / rep of the parent's slot, so 8 channels need 8 / rep elements
-// (one for rep >= 8): one 16-, 8-, 4- or 2-byte load, widened by repeating each element rep times.
-__device__ __forceinline__ u32x4 load_skip8(const __amdgpu_buffer_rsrc_t& rs, const ConvArgs& a, int src, int c8,
-                                            bool ok) {
-  const uint32_t s = (uint32_t)src;
-  const bool live = ok && s < a.skip_n * 8u;
-  const uint32_t base = (s >> 3) * (uint32_t)a.skip_cin + (s & 7u) * (uint32_t)(a.skip_cin >> 3) +
-                        (uint32_t)(c8 / a.skip_rep);
-  const uint32_t off = live ? base * 2u : kOutOfRange;
-  auto dup = [](uint32_t v16) { return (v16 & 0xffffu) | (v16 << 16); };
-  if (a.skip_rep == 1) return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-  if (a.skip_rep == 2) {
-    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-    const u32x2v q = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
-    return u32x4{dup(q[0]), dup(q[0] >> 16), dup(q[1]), dup(q[1] >> 16)};
-  }
-  if (a.skip_rep == 4) {
-    const uint32_t q = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
-    return u32x4{dup(q), dup(q), dup(q >> 16), dup(q >> 16)};
-  }
-  const uint32_t q = dup(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
-  return u32x4{q, q, q, q};
 }
 
 // Halo kernel (Co = 64; Ci = 32*S, used at Ci = 64): a workgroup owns a window of B consecutive rows of the input (spatial)
@@ -2202,7 +2223,6 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   if (b) REQ(b->numel() == Co && (b->dt == F32 || b->dt == F16 || b->dt == BF16), "bias must be [Co] f32/f16/bf16");
   if (N == 0) return;
   SpConvCfg cfg = spconv_cfg(N, Ci, Co);
-  const Tensor& code = c.block_masks(cfg.B1);
   Tensor bf;
   if (b) {
     if (b->dt == F32) bf = *b;
@@ -2222,7 +2242,6 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   a.nbr = c.nbr.ptr<uint32_t>();
   a.order = c.sorted.ptr<int32_t>();
   a.gray = c.gray.ptr<int32_t>();
-  a.code = code.ptr<uint32_t>();
   REQ((uint64_t)M * Ci * 2 <= kMaxBufferBytes && (uint64_t)Co * 27 * Ci * 2 <= kMaxBufferBytes,
       "x or w larger than %llu bytes", (unsigned long long)kMaxBufferBytes);
   a.x_bytes = (uint32_t)((uint64_t)M * Ci * 2);
@@ -2245,13 +2264,8 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   Tensor wpack, mtbl;
   REQ(!row_map || reads_row_table(cfg, Ci, Co, act), "row map with a kernel that reads nbr directly");
   const SpConvCache::HaloTable* ht = nullptr;
-  if (Co == 64 && Ci == 64 && halo_enabled()) {
-    ht = &c.halo_table(HaloShape<2>::B, HaloShape<2>::UM);
-    if (!ht->ok) ht = nullptr;
-  } else if (Co == 64 && Ci == 128 && halo128_enabled()) {
-    ht = &c.halo_table(HaloShape<4>::B, HaloShape<4>::UM);
-    if (!ht->ok) ht = nullptr;
-  }
+  if (Co == 64 && Ci == 64 && halo_enabled()) ht = &c.halo_table(HaloShape<2>::B, HaloShape<2>::UM);
+  else if (Co == 64 && Ci == 128 && halo128_enabled()) ht = &c.halo_table(HaloShape<4>::B, HaloShape<4>::UM);
   if (ht) {  // halo kernel: narrow weight order, the tile's distinct neighbour rows copied to LDS once
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w_narrow<<<dim3(Ci / 32, Co / 16, 27), 64, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Co, Ci);
@@ -2314,8 +2328,12 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       a.tsched = c.tile_schedule(-1, 128).ptr<int32_t>();
     }
   }
-  REQ(!skip || (ht && ht->spill_n == 0), "the fused skip residual needs the halo kernel with no spill tiles");
-  REQ(!ln || (ht && ht->spill_n == 0), "the fused pre-activation needs the halo kernel with no spill tiles");
+  REQ(!skip || ht, "the fused skip residual needs the halo kernel");
+  REQ(!ln || (ht && ht->host_spills() == 0), "the fused pre-activation needs the halo kernel with no spill tiles");
+  // the generic kernel reads the reference's per-block offset masks (valid(B1)'s OR masks); the others do not
+  if (!ht && !(Co == 64 && Ci <= 128) && !(Co % 256 == 0 && Ci % 64 == 0 && w256_enabled()) &&
+      !(cfg.BK == 64 && Co % 128 == 0))
+    a.code = c.block_masks(cfg.B1).ptr<uint32_t>();
   if (ln) {
     a.ln_on = 1;
     a.ln_gamma = ln->gamma ? ln->gamma->ptr<float>() : nullptr;
@@ -2323,26 +2341,23 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
     a.ln_eps = ln->eps;
     a.ln_act = ln->act;
   }
-  if (ht && ht->spill_n > 0) {
-    // The halo kernel skips the spill tiles; their positions go to the gathering kernel. It runs on a second stream
-    // beside the halo kernel (a few tiles of long latency; after it, it added ~36 us to C4's 0.64 ms): fork after
-    // everything both kernels read is queued on the library stream, join before anything later on it.
+  if (ht) {
+    // The halo kernel skips the spill tiles (their count is known only on the device); the gathering kernel computes
+    // them from the device list, with the identity row order inside each tile (tbl = nbr, gs = gray), on a second
+    // stream beside the halo kernel (a few tiles of long latency; after it, it added ~36 us to C4's 0.64 ms). Its
+    // grid covers every tile; workgroups past the spill count exit at once. Fork after everything both kernels read
+    // is queued on the library stream, join before anything later on it.
     ConvArgs sa = a;
     sa.hrows = nullptr;
     sa.hcount = nullptr;
     sa.hidx = nullptr;
     sa.hgm = nullptr;
-    sa.rmap = nullptr;
-    sa.N = (int)ht->spill_n;
-    sa.order = ht->spill.order.ptr<int32_t>();
-    sa.gs = ht->spill.gs.ptr<int32_t>();
-    sa.tbl = ht->spill.tbl.ptr<uint32_t>();
-    sa.tbl_bytes = (uint32_t)ht->spill.tbl.bytes();
-    if (row_map) {
-      mtbl = empty(ht->spill.tbl.sh, I32);
-      map_table_rows(ht->spill.tbl, *row_map, shift, M, mtbl);
-      sa.tbl = mtbl.ptr<uint32_t>();
-    }
+    sa.order = nullptr;
+    sa.gs = c.gray.ptr<int32_t>();
+    sa.tbl = c.nbr.ptr<uint32_t>();
+    sa.tbl_bytes = a.nbr_bytes;
+    sa.tlist = ht->spill_list.ptr<int32_t>();
+    sa.tcount = ht->spill_count.ptr<int32_t>();
     ktimer_mark();
     SideStream& ss = side_stream();
     CK(hipEventRecord(ss.fork, stream()));
@@ -2376,11 +2391,8 @@ void subm_conv_skip(const Tensor& x, const Tensor& w, const Tensor* b, int act, 
   REQ((rep & (rep - 1)) == 0, "Co / (Cin/8) = %d must be a power of two", rep);
   REQ((uint64_t)x_skip.bytes() <= kMaxBufferBytes && ((uintptr_t)x_skip.p % 16) == 0, "x_skip too large / unaligned");
   REQ(!(act & EPI_F16_COMPAT), "no fp16-compatible epilogue with the fused skip");
-  bool fused = c.N > 0 && Ci == 64 && Co == 64 && halo_enabled();
-  if (fused) {
-    const SpConvCache::HaloTable& ht = c.halo_table(HaloShape<2>::B, HaloShape<2>::UM);
-    fused = ht.ok && ht.spill_n == 0;
-  }
+  // 64 -> 64: the halo kernel (and the gathering kernel for its spill tiles) adds the skip rows in the epilogue
+  const bool fused = c.N > 0 && Ci == 64 && Co == 64 && halo_enabled();
   if (fused) {
     const SkipRes sk{&x_skip, &src};
     conv_impl(x, nullptr, 0, w, b, nullptr, act, c, out, &sk);
@@ -2451,7 +2463,7 @@ void subm_conv_preln(const Tensor& x_src, const Tensor* row_map, int shift, cons
   if (fused) {
     const SpConvCache::HaloTable& ht =
         Ci == 64 ? c.halo_table(HaloShape<2>::B, HaloShape<2>::UM) : c.halo_table(HaloShape<4>::B, HaloShape<4>::UM);
-    fused = ht.ok && ht.spill_n == 0;
+    fused = ht.host_spills() == 0;  // the gathering kernel of spill tiles has no pre-activation prologue
   }
   if (fused) {
     const PreLN pl{gamma, beta, eps, pre_act};

@@ -596,6 +596,7 @@ const Tensor& SpConvCache::window_order(int log2w) {
 // one contiguous range.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+typedef uint64_t u64x2_t __attribute__((ext_vector_type(2)));
 __global__ void __launch_bounds__(256) k_row_table(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ gray,
                                                    const int32_t* __restrict__ order, i64 nsrc, i64 n, i64 npad,
                                                    uint32_t* __restrict__ tbl, int32_t* __restrict__ gs) {
@@ -920,48 +921,94 @@ __global__ void k_fill_i32(int32_t* __restrict__ p, i64 n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
-// One workgroup per tile of B rows (positions of the tile order), one thread per row. The tile's neighbour rows go
-// into an LDS open-addressed set (linear probing, at most kHaloSlots probes: a tile with more distinct rows is
-// flagged); occupied slots are then numbered by a workgroup prefix count, which gives the halo list and every
-// (row, offset) its index in it. The list order follows the slots (not deterministic under concurrent inserts) --
-// only where a row sits in the conv's LDS copy depends on it, never a sum.
-template <int B, int UM>
-__global__ void __launch_bounds__(B) k_halo_build(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ order,
-                                                  i64 n, int32_t* __restrict__ rows, int32_t* __restrict__ count,
-                                                  uint16_t* __restrict__ idx, uint32_t* __restrict__ gm,
-                                                  int32_t* __restrict__ overflow) {
-  constexpr int NWV = B / 64, SPT = kHaloSlots / B;  // wavefronts, slots per thread
-  static_assert(B % 64 == 0 && B <= 256 && UM < 65535 && 2 * UM <= kHaloSlots, "halo tile shape");
-  // B-row windows (SpConvCache::window_order(log2 B)): tile t holds exactly the rows t*B .. t*B + B
+// One workgroup per tile = B consecutive rows r0 .. r0+B of the input order, one thread per row. In one launch, with
+// no host round trip, it
+//  * orders the window: each row's rank among the window's rows by decoded mask (binary value of its gray code),
+//    ties by row, which is the stable sort of the window (order[r0 + rank] = row; rows past n rank last);
+//  * collects the tile's distinct neighbour rows: a row within D rows of the window (r0-D .. r0+B+D; 95% of the
+//    (row, offset) entries on C4's shells for D = 512) marks a slot of a direct LDS flag array, any other goes into
+//    an LDS open-addressed set (linear probing); a prefix count over both numbers the halo (flagged rows first,
+//    ascending, then the set's slots) and gives every (row, offset) its index;
+//  * stores the halo row ids (rows[t*UM + u], -1 past the count), the (offset, tile position) -> index table, the
+//    16-position group masks and the count. A tile with more than UM distinct rows (or a full set) is a spill tile:
+//    count -1, and it is appended to spill_list (spill_count entries, the order of appends is immaterial: each spill
+//    tile is computed on its own by the gathering kernel).
+// Only where a row sits in the conv's LDS copy depends on the halo numbering, never a sum.
+template <int B, int UM, int D>
+__global__ void __launch_bounds__(B) k_halo_build(const uint32_t* __restrict__ nbr, const int32_t* __restrict__ gray,
+                                                  i64 n, int32_t* __restrict__ order, int32_t* __restrict__ rows,
+                                                  int32_t* __restrict__ count, uint16_t* __restrict__ idx,
+                                                  uint32_t* __restrict__ gm, int32_t* __restrict__ spill_list,
+                                                  int32_t* __restrict__ spill_count) {
+  constexpr int NWV = B / 64, SPT = kHaloSlots / B, R = B + 2 * D, RPT = R / B;
+  static_assert(B % 64 == 0 && B <= 256 && UM < 65535 && R % B == 0, "halo tile shape");
   __shared__ uint32_t keys[kHaloSlots];
   __shared__ int pos[kHaloSlots];
-  __shared__ __attribute__((aligned(16))) uint32_t nbL[B * 27];
-  __shared__ int wsum[NWV];
+  __shared__ int rpos[R];
+  __shared__ __attribute__((aligned(16))) uint64_t keyL[B];
+  __shared__ uint32_t maskL[B];
+  __shared__ int wsum[2][NWV];
   __shared__ int bad;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const i64 t = blockIdx.x, p = t * B + tid;  // position in the tile order; its row is order[p]
-  const i64 r = p < n ? order[p] : n;
-  // the tile order permutes rows inside B-row windows, so the tile's neighbour rows are the contiguous block
-  // nbr[t*B .. t*B + B): copied to LDS with 16-byte loads (27 strided 4-byte loads per thread touched 64 lines each)
-  const i64 r0 = t * B;
-  const int nw = (int)min<i64>(B, n - r0) * 27;
-  const uint4* src4 = (const uint4*)(nbr + r0 * 27);  // r0 * 108 bytes: 16-byte aligned (B % 4 == 0)
-  for (int i = tid; i < nw / 4; i += B) ((uint4*)nbL)[i] = src4[i];
-  for (int i = nw / 4 * 4 + tid; i < nw; i += B) nbL[i] = nbr[r0 * 27 + i];
-  for (int i = tid; i < kHaloSlots; i += B) keys[i] = EMPTY;
-  if (tid == 0) bad = 0;
-  __syncthreads();
-  const bool inwin = r >= r0 && r < r0 + B;  // always, for a window order; otherwise the tile is flagged
-  if (r < n && !inwin) bad = 1;
+  const i64 t = blockIdx.x, r0 = t * B, r = r0 + tid;
+  const bool live = r < n;
+  // the thread's own 108-byte nbr row straight into registers: 6 x 16 + 12 bytes (4-byte aligned buffer loads; a
+  // wavefront's loads cover one contiguous 6.9 KB range), EMPTY past n
   uint32_t nb[27];
-  int16_t sl[27];
-  uint32_t mask = 0;
+  {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(nbr), 0,
+                                                                        (int)min<i64>(n * 108, 0x7fffffff), 0x00020000);
+    const uint32_t o = live ? (uint32_t)r * 108u : 0x80000000u;
+#pragma unroll
+    for (int j = 0; j < 6; j++) {
+      const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(rs, o + j * 16, 0, 0);
+      nb[4 * j] = q[0];
+      nb[4 * j + 1] = q[1];
+      nb[4 * j + 2] = q[2];
+      nb[4 * j + 3] = q[3];
+    }
+    const u32x3_t q = __builtin_amdgcn_raw_buffer_load_b96(rs, o + 96, 0, 0);
+    nb[24] = q[0];
+    nb[25] = q[1];
+    nb[26] = q[2];
+  }
+  for (int i = tid; i < kHaloSlots; i += B) keys[i] = EMPTY;
+  for (int i = tid; i < R; i += B) rpos[i] = 0;
+  if (tid == 0) bad = 0;
+  const uint32_t g = live ? (uint32_t)gray[r] : 0u;
+  uint32_t bn = g;
+  bn ^= bn >> 1;
+  bn ^= bn >> 2;
+  bn ^= bn >> 4;
+  bn ^= bn >> 8;
+  bn ^= bn >> 16;
+  if (!live) bn = 0xffffffffu;  // past the end: after every live row
+  keyL[tid] = (uint64_t)bn << 8 | (uint32_t)tid;
+  __syncthreads();
+  // rank in the window: rows with a smaller decoded mask, or an equal one and a lower row (64-bit keys
+  // (mask << 8 | row in window) are distinct, so the rank is one comparison per row)
+  int rank = 0;
+  const uint64_t mine = (uint64_t)bn << 8 | (uint32_t)tid;
+#pragma unroll 16
+  for (int j = 0; j < B; j += 2) {
+    const u64x2_t q = *(const u64x2_t*)&keyL[j];
+    rank += (q[0] < mine) + (q[1] < mine);
+  }
+  if (live) order[r0 + rank] = (int32_t)r;
+  maskL[rank] = g;
+  int16_t sl[27];  // >= 0: hash slot; -1: EMPTY; -2 - d: direct flag d
+  const int lo = (int)r0 - D;
 #pragma unroll
   for (int v = 0; v < 27; v++) {
-    nb[v] = r < n && inwin ? nbL[(r - r0) * 27 + v] : EMPTY;
+    if (!live) nb[v] = EMPTY;
     sl[v] = -1;
     if (nb[v] == EMPTY) continue;
-    mask |= 1u << v;
+    const int d = (int)nb[v] - lo;
+    if (d >= 0 && d < R) {
+      rpos[d] = 1;
+      sl[v] = (int16_t)(-2 - d);
+      continue;
+    }
     uint32_t h = (nb[v] * 0x9e3779b1u) >> 22;  // 10 bits: kHaloSlots = 1024
     for (int probe = 0; probe < kHaloSlots; probe++, h = (h + 1) & (kHaloSlots - 1)) {
       const uint32_t prev = atomicCAS(&keys[h], EMPTY, nb[v]);
@@ -970,61 +1017,81 @@ __global__ void __launch_bounds__(B) k_halo_build(const uint32_t* __restrict__ n
         break;
       }
     }
-    if (sl[v] < 0) bad = 1;
+    if (sl[v] == -1) bad = 1;  // the set is full: the tile spills
   }
   __syncthreads();
-  // number the occupied slots: SPT per thread, wave prefix by shuffles, then the wave totals
-  int occ = 0;
+  // number the flagged rows (RPT per thread), then the occupied set slots (SPT per thread): wave prefix by shuffles,
+  // then the wave totals
+  int fo = 0, ho = 0;
 #pragma unroll
-  for (int k = 0; k < SPT; k++) occ += keys[tid * SPT + k] != EMPTY;
-  int incl = occ;
+  for (int k = 0; k < RPT; k++) fo += rpos[tid * RPT + k];
+#pragma unroll
+  for (int k = 0; k < SPT; k++) ho += keys[tid * SPT + k] != EMPTY;
+  int fi = fo, hi = ho;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
+    const int a = __shfl_up(fi, d, 64), b = __shfl_up(hi, d, 64);
+    if (lane >= d) {
+      fi += a;
+      hi += b;
+    }
   }
-  if (lane == 63) wsum[wv] = incl;
+  if (lane == 63) {
+    wsum[0][wv] = fi;
+    wsum[1][wv] = hi;
+  }
   __syncthreads();
-  int base = incl - occ, U = 0;
+  int fbase = fi - fo, hbase = hi - ho, UF = 0, UH = 0;
   for (int w = 0; w < NWV; w++) {
-    if (w < wv) base += wsum[w];
-    U += wsum[w];
+    if (w < wv) {
+      fbase += wsum[0][w];
+      hbase += wsum[1][w];
+    }
+    UF += wsum[0][w];
+    UH += wsum[1][w];
+  }
+  const int U = UF + UH;
+  hbase += UF;
+  int32_t* trow = rows + t * UM;
+#pragma unroll
+  for (int k = 0; k < RPT; k++) {
+    const int d = tid * RPT + k;
+    if (rpos[d]) {
+      if (fbase < UM) trow[fbase] = lo + d;
+      rpos[d] = fbase++;
+    }
   }
 #pragma unroll
   for (int k = 0; k < SPT; k++) {
-    const int s = tid * SPT + k;
-    pos[s] = base;
-    if (keys[s] != EMPTY) {
-      if (base < UM) rows[t * UM + base] = (int32_t)keys[s];
-      base++;
+    const int sidx = tid * SPT + k;
+    pos[sidx] = hbase;
+    if (keys[sidx] != EMPTY) {
+      if (hbase < UM) trow[hbase] = (int32_t)keys[sidx];
+      hbase++;
     }
   }
-  for (int u = U + tid; u < UM; u += B) rows[t * UM + u] = -1;  // unused slots: the conv loads them unconditionally
-  __syncthreads();
+  for (int u = U + tid; u < UM; u += B) trow[u] = -1;  // unused slots: the conv loads them unconditionally
+  __syncthreads();  // numbering done
+  // the (offset, tile position) -> index table: column `rank` of the tile's [27][B] block (positions past n hold
+  // the zero row: their rows rank last)
+  uint16_t* it = idx + t * 27 * B + rank;
 #pragma unroll
   for (int v = 0; v < 27; v++) {
     int u = UM;  // EMPTY: the zero row
-    if (sl[v] >= 0) u = min(pos[sl[v]], UM);
-    idx[(t * 27 + v) * B + tid] = (uint16_t)u;
+    if (sl[v] >= 0) u = pos[sl[v]];
+    else if (sl[v] <= -2) u = rpos[-2 - sl[v]];
+    it[v * B] = (uint16_t)min(u, UM);
   }
-  // 16-row group masks
+  // 16-position group masks (tile order)
+  uint32_t mk = maskL[tid];
 #pragma unroll
-  for (int d = 1; d < 16; d <<= 1) mask |= (uint32_t)__shfl_xor((int)mask, d, 64);
-  if ((tid & 15) == 0) gm[t * (B / 16) + tid / 16] = mask;
+  for (int d = 1; d < 16; d <<= 1) mk |= (uint32_t)__shfl_xor((int)mk, d, 64);
+  if ((tid & 15) == 0) gm[t * (B / 16) + tid / 16] = mk;
   if (tid == 0) {
-    count[t] = U > UM ? -1 : U;  // a spill tile: served by the gathering kernel
-    if (bad) atomicMax(&overflow[0], 1);
-    if (U > UM) atomicAdd(&overflow[1], 1);
+    const bool spill = U > UM || bad;
+    count[t] = spill ? -1 : U;  // a spill tile: served by the gathering kernel
+    if (spill) spill_list[atomicAdd(spill_count, 1)] = (int32_t)t;
   }
-}
-
-// Positions of the spill tiles, in tile order: out[j*B + r] = order[tiles[j]*B + r] for positions below n.
-__global__ void k_spill_order(const int32_t* __restrict__ order, const int32_t* __restrict__ tiles, int k, int B, i64 n,
-                              int32_t* __restrict__ out) {
-  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (i64)k * B) return;
-  const i64 pos = (i64)tiles[i / B] * B + i % B;
-  if (pos < n) out[i] = order[pos];
 }
 }  // namespace
 
@@ -1032,48 +1099,31 @@ const SpConvCache::HaloTable& SpConvCache::halo_table(int B, int UM) {
   auto it = halo.find({B, UM});
   if (it != halo.end()) return it->second;
   HaloTable h;
+  REQ((i64)N * 108 < (1ll << 31), "halo schedule: %d rows (at most %lld)", N, (long long)((1ll << 31) / 108));
   const i64 tiles = std::max<i64>(cdiv(N, B), 1);
-  int log2b = 0;
-  while ((1 << log2b) < B) log2b++;
-  REQ((1 << log2b) == B, "halo tile rows %d: a power of two", B);
-  h.order = window_order(log2b);  // B-row windows of the input order, gray-sorted inside (tight 16-row masks)
+  h.tiles = tiles;
+  h.order = empty({std::max<i64>(N, 1)}, I32);  // B-row windows of the input order, gray-sorted inside
   h.rows = empty({tiles * UM}, I32);
   h.count = empty({tiles}, I32);
   h.idx = empty({tiles * 27 * B / 2}, I32);  // u16 entries
   h.gm = empty({tiles * (B / 16)}, I32);
-  Tensor flag = empty({2}, I32);  // [0]: the order is not a window order, [1]: spill tiles
-  k_fill_i32<<<1, 64, 0, stream()>>>(flag.ptr<int32_t>(), 2, 0);
+  h.spill_list = empty({tiles}, I32);
+  h.spill_count = empty({1}, I32);
+  k_fill_i32<<<1, 64, 0, stream()>>>(h.spill_count.ptr<int32_t>(), 1, 0);
   auto go = [&](auto kern) {
-    kern<<<(unsigned)tiles, B, 0, stream()>>>(nbr.ptr<uint32_t>(), h.order.ptr<int32_t>(), N, h.rows.ptr<int32_t>(),
-                                              h.count.ptr<int32_t>(), (uint16_t*)h.idx.p, h.gm.ptr<uint32_t>(),
-                                              flag.ptr<int32_t>());
+    kern<<<(unsigned)tiles, B, 0, stream()>>>(nbr.ptr<uint32_t>(), gray.ptr<int32_t>(), N, h.order.ptr<int32_t>(),
+                                              h.rows.ptr<int32_t>(), h.count.ptr<int32_t>(), (uint16_t*)h.idx.p,
+                                              h.gm.ptr<uint32_t>(), h.spill_list.ptr<int32_t>(),
+                                              h.spill_count.ptr<int32_t>());
   };
-  if (B == 256 && UM == 512) go(k_halo_build<256, 512>);
-  else if (B == 128 && UM == 256) go(k_halo_build<128, 256>);
+  if (B == 256 && UM == 512) go(k_halo_build<256, 512, 512>);
+  else if (B == 128 && UM == 256) go(k_halo_build<128, 256, 256>);
   else REQ(false, "no halo builder for B=%d UM=%d", B, UM);
   CK(hipGetLastError());
-  const auto fl = to_host_vec<int32_t>(flag);  // one host sync per cache and shape
-  h.ok = fl[0] == 0;
-  if (h.ok && fl[1] > 0) {  // spill tiles: their positions become a row table for the gathering kernel
-    const auto cnt = to_host_vec<int32_t>(h.count);
-    std::vector<int32_t> list;
-    for (i64 t = 0; t < tiles; t++)
-      if (cnt[t] < 0) list.push_back((int32_t)t);
-    REQ((i64)list.size() == fl[1], "spill tiles %zu, flagged %d", list.size(), fl[1]);
-    const int k = (int)list.size();
-    Tensor tl = from_host(list.data(), {k}, I32);
-    const i64 last = list.back();
-    h.spill_n = (i64)k * B - ((last + 1) * B > N ? (last + 1) * B - N : 0);  // only the last tile can be partial
-    h.spill.order = empty({(i64)k * B}, I32);
-    k_spill_order<<<cdiv((i64)k * B, 256), 256, 0, stream()>>>(h.order.ptr<int32_t>(), tl.ptr<int32_t>(), k, B, N,
-                                                               h.spill.order.ptr<int32_t>());
-    const i64 npad = cdiv(h.spill_n, kRowTablePad) * (i64)kRowTablePad;
-    h.spill.tbl = empty({npad, 27}, I32);
-    h.spill.gs = empty({npad}, I32);
-    k_row_table<<<cdiv(npad, 256), 256, 0, stream()>>>(nbr.ptr<uint32_t>(), gray.ptr<int32_t>(),
-                                                            h.spill.order.ptr<int32_t>(), N, h.spill_n, npad,
-                                                            h.spill.tbl.ptr<uint32_t>(), h.spill.gs.ptr<int32_t>());
-    CK(hipGetLastError());
-  }
   return halo.emplace(std::make_pair(B, UM), h).first->second;
+}
+
+int SpConvCache::HaloTable::host_spills() const {
+  if (spills_host < 0) spills_host = to_host_vec<int32_t>(spill_count)[0];  // one host sync, on first request
+  return spills_host;
 }

@@ -49,18 +49,18 @@ struct SpConvCache {
   // row_table(log2w).tbl with every non-EMPTY entry r replaced by row_map[r] >> shift, or EMPTY when that is not
   // below m (not memoized: row_map is the caller's). Used by the gathered conv.
   Tensor mapped_table(int log2w, const Tensor& row_map, int shift, i64 m);
-  // Halo schedule for the 64-output-channel convs: tiles of B consecutive entries of order = window_order(log2 B)
-  // (B-row windows of the input order, gray-sorted inside). Per tile: the distinct neighbour rows it reads
-  // (rows[t*UM + u], u < count[t]), each position's 27 neighbours as indices into that list (idx[(t*27 + v)*B + j],
-  // u16; UM = EMPTY, a zero row) and the per-16-position neighbour masks (gm[t*B/16 + g]). A tile that reads more
-  // than UM distinct rows is a spill tile: count[t] = -1 (the halo kernel skips it) and its positions go, in tile
-  // order, into `spill` (a row table of spill_n positions for the gathering kernel). ok = false only when the order
-  // is not a window order. Built on first use per (B, UM), one host sync, memoized.
+  // Halo schedule for the 64-output-channel convs: tiles of B consecutive rows of the input order, gray-sorted inside
+  // (order). Per tile: the distinct neighbour rows it reads (rows[t*UM + u], u < count[t]), each position's 27
+  // neighbours as indices into that list (idx[(t*27 + v)*B + j], u16; UM = EMPTY, a zero row) and the per-16-position
+  // neighbour masks (gm[t*B/16 + g]). A tile that reads more than UM distinct rows is a spill tile: count[t] = -1 (the
+  // halo kernel skips it) and its index is in spill_list (spill_count entries, on the device; the gathering kernel
+  // computes those tiles). Built on first use per (B, UM) in one launch with no host sync, memoized.
   struct HaloTable {
     Tensor order, rows, count, idx, gm;
-    RowTable spill;
-    i64 spill_n = 0;
-    bool ok = false;
+    Tensor spill_list, spill_count;  // spill tiles (device list, device count)
+    i64 tiles = 0;
+    mutable int spills_host = -1;
+    int host_spills() const;  // the spill count on the host (syncs once; only the opt-in one-kernel pre-activation asks)
   };
   std::map<std::pair<int, int>, HaloTable> halo;
   const HaloTable& halo_table(int B, int UM);
