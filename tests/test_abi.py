@@ -80,3 +80,17 @@ int main(void) {
     assert os.system(cmd) == 0, cmd
     out = os.popen(str(exe)).read()
     assert out.strip() == "128 64 1"
+
+
+def test_diagnostics_without_gpu():
+    """The timing and allocation diagnostics need no device: no conv call -> no kernel times; null pointers are
+    errors; the allocation counters are readable."""
+    lib = spconv_amd.load_library()
+    assert lib.spc_kernel_timing(1) == 0
+    n = ctypes.c_int(-1)
+    assert lib.spc_kernel_times(None, 0, ctypes.byref(n)) == 0 and n.value == 0
+    assert lib.spc_kernel_timing(0) == 0
+    assert lib.spc_kernel_times(None, 0, None) == -1
+    req, drv = spconv_amd.alloc_counts()
+    assert req >= drv >= 0
+    assert lib.spc_alloc_counts(None, None) == -1

@@ -649,3 +649,25 @@ def test_c5_conv_skip_full(gpu):
     assert rel2 <= 2e-3 and np.all(np.abs(y2r - ref) <= np.maximum(2e-2, 2 * ulp(ref, "bf16"))), \
         f"conv + add_skip: rel-L2 {rel2:.3g}"
     assert np.linalg.norm(yr - ref) <= np.linalg.norm(y2r - ref) * 1.01, "one rounding should not be worse than two"
+
+
+def test_kernel_timing(gpu):
+    """spc_kernel_timing brackets each conv call's conv kernels with events: one time per call, positive, below the
+    host-timed call including the weight repack; off again, calls add no records."""
+    import time
+    c = shell(10.0)
+    cache = sp.build_neighbors(torch.from_numpy(c).to(gpu))
+    x = torch.randn((len(c), 256), device=gpu).to(torch.bfloat16)
+    w = (torch.randn((256, 27, 256), device=gpu) / 83).to(torch.bfloat16)
+    y = sp.subm_conv_fused(x, w, None, cache)
+    torch.cuda.synchronize()
+    sp.kernel_timing(True)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        sp.subm_conv_fused(x, w, None, cache, out=y)
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) * 1e3
+    sp.kernel_timing(False)
+    sp.subm_conv_fused(x, w, None, cache, out=y)
+    t = sp.kernel_times()
+    assert len(t) == 3 and all(v > 0 for v in t) and sum(t) <= host_ms, (t, host_ms)
