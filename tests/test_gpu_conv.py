@@ -671,3 +671,13 @@ def test_kernel_timing(gpu):
     sp.subm_conv_fused(x, w, None, cache, out=y)
     t = sp.kernel_times()
     assert len(t) == 3 and all(v > 0 for v in t) and sum(t) <= host_ms, (t, host_ms)
+
+
+@pytest.mark.parametrize("ci,co,r", [(1024, 1024, 6.0), (1024, 4096, 5.0), (512, 512, 8.0), (512, 2048, 7.0),
+                                     (256, 1024, 9.0), (128, 128, 12.0), (128, 512, 11.0)])
+def test_decoder_level_widths(gpu, ci, co, r):
+    """The sparse decoders' layer widths (C = 1024 -> 512 -> 256 -> 128 -> 64; ConvNeXt convs C -> C and up-convs
+    C -> 8 * C/2, as the reference's autotune keys list them, e.g. (2^11, 1024, 4096, 27)), on small shells: fp32
+    output against the oracle, bf16 output = round(fp32 output). These shapes take the wide kernels' split schedules
+    (few rows, many channels)."""
+    run_case(gpu, shell(r), ci, co, act=1, res_dt="bf16", seed=int(r))
