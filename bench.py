@@ -388,6 +388,46 @@ def measure(name, args, torch, np, sp, W, cpu, want_cpu, cpu_seconds, extras):
     return out
 
 
+# The sparse decoders' conv shapes beyond the five configs: (log2 N, Ci, Co) from the reference's autotune keys
+# (assets/flexgemm_autotune.json: ConvNeXt convs C -> C and up-convs C -> 8 * C/2 at each level, N from 2^11 at
+# C = 1024 to 2^21 at C = 64).
+DECODER_LEVELS = [(11, 1024, 1024), (11, 1024, 4096), (14, 512, 512), (14, 512, 2048), (16, 256, 256),
+                  (16, 256, 1024), (19, 128, 128), (19, 128, 512), (21, 64, 64)]
+
+
+def decoder_levels(torch, np, sp, W):
+    """Conv kernel time at each decoder level's shape on a seeded shell of ~2^L voxels (the c3 recipe with the grid
+    scaled to the voxel count), bias + SiLU, bf16; HIP events around the conv kernels, median of 20 calls."""
+    dev = torch.device("cuda:0")
+    out = []
+    for L, ci, co in DECODER_LEVELS:
+        G = max(16, int(256 * ((1 << L) / 390500) ** 0.5))
+        cfg = W.Config("level", G, 12, (20 * G / 256, 90 * G / 256), True, 0.8, ci, co, "bf16", "bias+silu", 7000 + L)
+        c = torch.from_numpy(W.shell_coords(cfg)).to(dev)
+        n = c.shape[0]
+        cache = sp.build_neighbors(c)
+        P = int((cache.tensors()[0] != -1).sum().item())
+        g = torch.Generator(device=dev)
+        g.manual_seed(cfg.seed)
+        x = torch.randn((n, ci), generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn((co, 27, ci), generator=g, device=dev) / (27 * ci) ** 0.5).to(torch.bfloat16)
+        b = torch.randn((co,), generator=g, device=dev) * 0.1
+        y = torch.empty((n, co), dtype=torch.bfloat16, device=dev)
+        for _ in range(10):
+            sp.subm_conv_fused(x, w, b, cache, act=sp.ACT_SILU, out=y)
+        sp.kernel_timing(True)
+        for _ in range(20):
+            sp.subm_conv_fused(x, w, b, cache, act=sp.ACT_SILU, out=y)
+        sp.kernel_timing(False)
+        kt = float(np.median(sp.kernel_times()))
+        fl = 2.0 * P * ci * co
+        out.append({"log2N": L, "N": n, "Ci": ci, "Co": co, "active_pairs": P, "kernel_ms": round(kt, 4),
+                    "tflops": round(fl / (kt * 1e-3) / 1e12, 1),
+                    "frac_of_mfma_peak": round(fl / (kt * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)})
+        del cache, x, w, y
+    return out
+
+
 def c1_cpu(np, W, cpu, seconds):
     """Config c1 runs on the CPU only: 32^3 shell, 32 -> 32 fp32 with bias, the oracle's kernel map and conv over
     every row (repeated to fill ~`seconds`)."""
@@ -501,6 +541,8 @@ def main():
                                        True)
         if not args.no_cpu:
             others["c1"] = c1_cpu(np, W, cpu, args.cpu_seconds_extra)
+        torch.cuda.empty_cache()
+        levels = decoder_levels(torch, np, sp, W)
 
     r = head["roofline"]
     cfg = {k: head[k] for k in ("workload", "N", "Ci", "Co", "active_pairs")}
@@ -517,7 +559,7 @@ def main():
                                        "achieved_step", "frac_step")},
         "cpu_baseline": head.get("cpu_baseline"),
         "extras": dict(keep, roofline_detail=r, measured_peaks=measured, configs=others, source_digest=args.digest,
-                       host_cpu=cpu),
+                       host_cpu=cpu, decoder_levels=levels if extras else None),
     }
     print(json.dumps(out), flush=True)
 
