@@ -222,6 +222,13 @@ int spc_kernel_times(float* ms, int max, int* n);
  * reference: a diagnostic for callers that must not allocate (compare the counts around a call). Host only. */
 int spc_alloc_counts(int64_t* requests, int64_t* driver_allocs);
 
+/* Returns the library's cached, currently unused device blocks to the driver (the library keeps freed blocks for
+ * reuse, as a framework's caching allocator does) and trims the device memory pools; waits for the devices those
+ * blocks belong to. *bytes (may be NULL) receives the bytes released. Blocks held by live caches are untouched.
+ * Replaces: nothing in the reference, whose allocator frees on release (src/core.cu:32-40); for pipelines that run
+ * other large models between decoder passes. */
+int spc_release_cached_memory(int64_t* bytes);
+
 int spc_subdivide_noalloc(const int32_t* coords, const uint16_t* logits_f16, int64_t n, int32_t* child_coords,
                           int32_t* src, int64_t* m_dev);
 

@@ -312,3 +312,24 @@ def test_subdivide_build(gpu, name):
     # no parents: empty level
     e_cc, e_src, e_cache = sp.subdivide_build(tc[:0], tl[:0])
     assert e_cc.shape == (0, 4) and e_src.shape == (0,) and e_cache.N == 0
+
+
+def test_release_cached_memory(gpu):
+    """Cached blocks go back to the driver: after a cache is dropped its buffers are cached; releasing them reports
+    their bytes, the next build allocates from the driver again, and its map is unchanged."""
+    import gc
+    sp.set_stream(torch.cuda.current_stream())
+    c = torch.from_numpy(W.shell_coords(W.CONFIGS["c1"])).to(gpu)
+    a = sp.build_neighbors(c)
+    ref = [t.clone() for t in a.tensors()]
+    del a
+    gc.collect()
+    torch.cuda.synchronize()
+    assert sp.release_cached_memory() > 0
+    assert sp.release_cached_memory() == 0
+    _, drv0 = sp.alloc_counts()
+    b = sp.build_neighbors(c)
+    _, drv1 = sp.alloc_counts()
+    assert drv1 > drv0
+    for x, y in zip(ref, b.tensors()):
+        assert torch.equal(x, y)

@@ -293,6 +293,13 @@ SPC_API int spc_kernel_times(float* ms, int max, int* n) {
   });
 }
 
+SPC_API int spc_release_cached_memory(int64_t* bytes) {
+  return guarded([&] {
+    const i64 b = release_cached_memory();
+    if (bytes) *bytes = b;
+  });
+}
+
 SPC_API int spc_alloc_counts(int64_t* requests, int64_t* driver_allocs) {
   return guarded([&] {
     REQ(requests && driver_allocs, "null argument");

@@ -73,6 +73,9 @@ Tensor zeros(std::vector<i64> sh, DT dt);
 // Device allocations the library has made since the process started: every request to empty() with a nonzero size
 // (served from the free lists or not), and the hipMallocAsync calls among them.
 void alloc_counts(i64* requests, i64* driver_allocs);
+// Frees every cached (currently unused) device block back to the driver and trims the devices' memory pools: waits
+// for the devices the blocks belong to. Blocks still owned by live tensors are untouched. Returns the bytes freed.
+i64 release_cached_memory();
 Tensor from_host(const void* src, std::vector<i64> sh, DT dt);
 std::vector<char> to_host(const Tensor& t);
 template <class T>

@@ -1,5 +1,6 @@
 #include "core.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <mutex>
@@ -111,6 +112,37 @@ Tensor empty(std::vector<i64> sh, DT dt) {
   }
   return t;
 }
+i64 release_cached_memory() {
+  std::map<BlockKey, std::vector<void*>> lists;
+  {
+    std::lock_guard<std::mutex> g(g_alloc_mu);
+    lists.swap(free_blocks());
+  }
+  i64 bytes = 0;
+  std::vector<int> devs;
+  bool any = false;
+  for (auto& kv : lists) any |= !kv.second.empty();
+  if (!any) return 0;
+  int cur = 0;
+  CK(hipGetDevice(&cur));
+  for (auto& kv : lists) {
+    if (kv.second.empty()) continue;
+    CK(hipSetDevice(kv.first.dev));
+    for (void* p : kv.second) CK(hipFreeAsync(p, kv.first.stream));  // stream-ordered after the block's last use
+    bytes += (i64)kv.first.size * (i64)kv.second.size();
+    if (std::find(devs.begin(), devs.end(), kv.first.dev) == devs.end()) devs.push_back(kv.first.dev);
+  }
+  for (int d : devs) {  // hand the freed memory back to the device (the pool keeps it otherwise)
+    CK(hipSetDevice(d));
+    CK(hipDeviceSynchronize());
+    hipMemPool_t pool;
+    CK(hipDeviceGetDefaultMemPool(&pool, d));
+    CK(hipMemPoolTrimTo(pool, 0));
+  }
+  CK(hipSetDevice(cur));
+  return bytes;
+}
+
 void alloc_counts(i64* requests, i64* driver_allocs) {
   *requests = g_alloc_requests.load();
   *driver_allocs = g_driver_allocs.load();

@@ -30,7 +30,8 @@ SYMBOLS = ("spc_last_error", "spc_set_stream", "spc_build_neighbors", "spc_build
            "spc_conv_cfg_autotune", "spc_conv_cfg_autotune_strict", "spc_subm_conv", "spc_subm_conv_fused", "spc_subm_conv_gathered",
            "spc_gather_ln_act", "spc_add_skip", "spc_convnext_mlp", "spc_subm_conv_skip",
            "spc_subdivide", "spc_subdivide_noalloc", "spc_subm_conv_replay", "spc_grid_sample_map",
-           "spc_grid_sample_sum", "spc_subdivide_build", "spc_subm_conv_preln", "spc_alloc_counts", "spc_kernel_timing", "spc_kernel_times")
+           "spc_grid_sample_sum", "spc_subdivide_build", "spc_subm_conv_preln", "spc_alloc_counts", "spc_kernel_timing",
+           "spc_kernel_times", "spc_release_cached_memory")
 
 _lib = None
 
@@ -77,6 +78,7 @@ def load_library():
                                       P, P]
     L.spc_alloc_counts.argtypes = [ctypes.POINTER(I64), ctypes.POINTER(I64)]
     L.spc_kernel_timing.argtypes = [I]
+    L.spc_release_cached_memory.argtypes = [ctypes.POINTER(I64)]
     L.spc_kernel_times.argtypes = [ctypes.POINTER(ctypes.c_float), I, ctypes.POINTER(I)]
     for name in SYMBOLS:
         if name != "spc_last_error":
@@ -445,6 +447,13 @@ def kernel_times():
     buf = (ctypes.c_float * max(n.value, 1))()
     _check(L.spc_kernel_times(buf, n.value, ctypes.byref(n)))
     return list(buf[:n.value])
+
+
+def release_cached_memory() -> int:
+    """Return the library's cached, unused device blocks to the driver; the bytes released."""
+    b = ctypes.c_int64()
+    _check(load_library().spc_release_cached_memory(ctypes.byref(b)))
+    return b.value
 
 
 def alloc_counts():
