@@ -960,8 +960,8 @@ __global__ void __launch_bounds__(B) k_halo_build(const uint32_t* __restrict__ n
   uint32_t nb[27];
   {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(nbr), 0,
-                                                                        (int)min<i64>(n * 108, 0x7fffffff), 0x00020000);
-    const uint32_t o = live ? (uint32_t)r * 108u : 0x80000000u;
+                                                                        (int)(uint32_t)(n * 108), 0x00020000);
+    const uint32_t o = live ? (uint32_t)r * 108u : 0xffff0000u;  // past the end: zeros
 #pragma unroll
     for (int j = 0; j < 6; j++) {
       const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(rs, o + j * 16, 0, 0);
@@ -1102,7 +1102,7 @@ const SpConvCache::HaloTable& SpConvCache::halo_table(int B, int UM) {
   auto it = halo.find({B, UM});
   if (it != halo.end()) return it->second;
   HaloTable h;
-  REQ((i64)N * 108 < (1ll << 31), "halo schedule: %d rows (at most %lld)", N, (long long)((1ll << 31) / 108));
+  REQ((i64)N * 108 <= 0xfffe0000ll, "halo schedule: %d rows (at most %lld)", N, 0xfffe0000ll / 108);
   const i64 tiles = std::max<i64>(cdiv(N, B), 1);
   h.tiles = tiles;
   h.order = empty({std::max<i64>(N, 1)}, I32);  // B-row windows of the input order, gray-sorted inside
