@@ -263,7 +263,9 @@ __global__ void __launch_bounds__(NVV) k_neighbors_vox(const int4* __restrict__ 
 #pragma unroll
   for (int k = 0; k < 27; k++) {
     const int i = k * NVV + tid;
-    if (i < tot) o[i] = rows[i];
+    // non-temporal: the 108-byte rows are not read again in this build, and kept in L2 they would evict the brick
+    // records and table lines the neighbour queries read (C4 build 0.477 -> 0.421 ms, C5's children 0.330 -> 0.315)
+    if (i < tot) __builtin_nontemporal_store(rows[i], &o[i]);
   }
 }
 
