@@ -36,7 +36,7 @@ class Config:
     keep_frac: float = 0.0
 
 
-# The five BASELINE configurations. Shape counts, radii and dtypes are the stated ones. Where a config states the
+# The five benchmark configurations. Shape counts, radii and dtypes are the stated ones. Where a config states the
 # shell thickness it is used as stated: c2 |sdf| <= 1 (h = 1.0; 10 842 voxels with this seed, below the quoted
 # ~25k), c4 a 1-voxel shell (h = 0.5; 3.76 M voxels, P/N = 10.5). Where it does not (c1 ~5k, c3 ~400k, c5 ~800k
 # parents) h is chosen so the count lands near the stated size. Counts are whatever the seed gives.
