@@ -715,6 +715,11 @@ __global__ void __launch_bounds__(64) k_pack_w_narrow(const u32x4* __restrict__ 
 //    MFMAs for it. Rows come in the order the caller chooses (null = identity); the spatial (Morton) order keeps
 //    the gathers of neighbouring rows in L2.
 //  * Epilogue: per 16-row group, accumulators go through LDS and leave as 16-byte segments of whole output rows.
+//  * LITE (used at Ci = 128, G = 2): the gathers run one offset ahead instead of two, the weight fragments are read
+//    from LDS per K step, and residuals are loaded in the epilogue instead of staged in LDS -- 158 VGPRs and 47 KB of
+//    LDS, so three workgroups per CU instead of two. The gathers are served from the MALL and the loop waits on
+//    them; a third workgroup hides more than the second offset of look-ahead did (C5 children 0.907 -> 0.856 ms;
+//    two offsets ahead with the other savings, still two workgroups per CU: 0.923). Same sums, same bits.
 // Copies rows [row0, row0+BM) of the tile-ordered neighbour table (27 u32 per row, contiguous) into LDS by DMA:
 // 16 bytes per lane, so each wavefront instruction moves 1 KiB with no registers involved.
 template <int BM, int NT>
@@ -760,15 +765,15 @@ __device__ __forceinline__ u32x4 load_skip8(const __amdgpu_buffer_rsrc_t& rs, co
   return u32x4{q, q, q, q};
 }
 
-template <bool F16, int S, int T, int G>
-__global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
+template <bool F16, int S, int T, int G, bool LITE = false>
+__global__ void __launch_bounds__(256, LITE ? 3 : 1) k_conv_narrow(ConvArgs a) {
   constexpr int NT = 256, BM = 4 * 16 * G, CI = 32 * S, CO = 16 * T, WB = T * S * 64;  // WB: 16B units per offset
   static_assert(WB % NT == 0, "weight slice split");
   __shared__ __attribute__((aligned(16))) u32x4 Bs[2][WB];
   constexpr int SR = 27;  // srcT row stride: the table's 27 neighbour indices per row
   __shared__ __attribute__((aligned(16))) uint32_t srcT[BM * SR];
   __shared__ int ordT[BM];
-  __shared__ __attribute__((aligned(16))) u32x4 resL[BM * CO * 2 / 16];
+  __shared__ __attribute__((aligned(16))) u32x4 resL[LITE ? 1 : BM * CO * 2 / 16];
   __shared__ uint32_t gmask[BM / 16];
   __shared__ int vlist[32];
 
@@ -854,6 +859,21 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
     const int vn = __builtin_amdgcn_readfirstlane(vlist[vi + 2 < nvv ? vi + 2 : nvv - 1]);
 #pragma unroll
     for (int k = 0; k < BL; k++) rbL[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, vn * WB * 16, 0);
+    if constexpr (LITE) {  // weight fragments read per K step: T instead of T x S live at once
+#pragma unroll
+      for (int m = 0; m < S; m++) {
+        u32x4 fb[T];
+#pragma unroll
+        for (int t = 0; t < T; t++) fb[t] = Bs[buf][(t * S + m) * 64 + lane];
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+          if ((gms[i] >> v) & 1u) {
+#pragma unroll
+            for (int t = 0; t < T; t++) acc[i][t] = mfma16<F16>(ra[i][m], fb[t], acc[i][t]);
+          }
+        }
+      }
+    } else {
     u32x4 fb[T][S];
 #pragma unroll
     for (int t = 0; t < T; t++)
@@ -868,6 +888,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
           for (int t = 0; t < T; t++) acc[i][t] = mfma16<F16>(ra[i][m], fb[t][m], acc[i][t]);
       }
     }
+    }
 #pragma unroll
     for (int k = 0; k < BL; k++) Bs[buf ^ 1][k * NT + tid] = rbS[k];
     __syncthreads();
@@ -879,7 +900,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
   // latency hides behind the loop; no registers held). Rows past N read out of range and land as zeros.
   constexpr int RU = BM * CO * 2 / 16, RK = RU / NT;  // 16-byte units, DMA loads per lane
   static_assert(RK * NT == RU, "residual tile split");
-  const bool res16 = a.res && a.res_dt != F32 && !a.skip_src;  // (a skip residual is loaded in the epilogue)
+  const bool res16 = !LITE && a.res && a.res_dt != F32 && !a.skip_src;  // (skip residual: loaded in the epilogue)
   if (res16) {
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, a.res_bytes);
 #pragma unroll
@@ -901,6 +922,21 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
 #pragma unroll
       for (int k = 0; k < BL; k++) rb[1][k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (k * NT + tid) * 16, v1 * WB * 16, 0);
     }
+    if constexpr (LITE) {  // gathers one entry ahead (two buffers)
+      u32x4 ra[2][G][S];
+      gather(0, ra[0]);
+      __syncthreads();
+      for (int vb = 0; vb < nvv; vb += 2) {
+        static_for<2>([&](auto J) __attribute__((always_inline)) {
+          constexpr int j = decltype(J)::value;
+          const int vi = vb + j;
+          if (vi < nvv) {
+            if (vi + 1 < nvv) gather(vi + 1, ra[(j + 1) % 2]);
+            compute(vi, j & 1, ra[j % 2], rb[j & 1], rb[(j + 1) & 1]);
+          }
+        });
+      }
+    } else {
     u32x4 ra[3][G][S];
     gather(0, ra[0]);
     if (nvv > 1) gather(1, ra[1]);
@@ -916,6 +952,7 @@ __global__ void __launch_bounds__(256) k_conv_narrow(ConvArgs a) {
           compute(vi, j & 1, ra[j % 3], rb[j & 1], rb[(j + 1) & 1]);
         }
       });
+    }
     }
   }
 
@@ -1269,7 +1306,9 @@ void launch_narrow(ConvArgs a, hipStream_t st = stream()) {
   a.tiles_m = cdiv(a.N, 4 * 16 * G);
   a.tiles_n = 1;
   a.grid = (a.tiles_m + 7) / 8 * 8;
-  k_conv_narrow<F16, S, T, G><<<a.grid, 256, 0, st>>>(a);
+  // Ci = 128: the three-workgroups-per-CU form (see k_conv_narrow)
+  if constexpr (S == 4) k_conv_narrow<F16, S, T, G, true><<<a.grid, 256, 0, st>>>(a);
+  else k_conv_narrow<F16, S, T, G><<<a.grid, 256, 0, st>>>(a);
 }
 
 // Wide-channel kernel, BM sorted rows x 256 channels per workgroup (4 wavefronts, each all BM rows x 64 channels =
