@@ -592,6 +592,23 @@ def test_w256_widths(gpu, monkeypatch, ci, co):
     run_case(gpu, c, ci, co, in_dt="f16", out_dt="f16", act=0, res_dt="f32", seed=4)
 
 
+def test_c3_w8_kernel(gpu, monkeypatch):
+    """The 8-wavefront 256 x 256 kernel with both operands in LDS (SPCONV_W8=1) on the full C3 workload, every row
+    against the oracle."""
+    monkeypatch.setenv("SPCONV_W8", "1")
+    cfg = W.CONFIGS["c3"]
+    run_case(gpu, W.shell_coords(cfg), cfg.ci, cfg.co, act=1, seed=cfg.seed)
+
+
+@pytest.mark.parametrize("ci,co", [(256, 256), (32, 256), (96, 512), (768, 768)])
+def test_w8_widths(gpu, monkeypatch, ci, co):
+    """8-wavefront 256 x 256 kernel on a small shell (ragged last tile) and every epilogue."""
+    monkeypatch.setenv("SPCONV_W8", "1")
+    c = shell(10.0)
+    run_case(gpu, c, ci, co, act=1, res_dt="bf16", seed=3)
+    run_case(gpu, c, ci, co, in_dt="f16", out_dt="f16", act=0, res_dt="f32", seed=4)
+
+
 def test_c5_gathered_full(gpu):
     """The timed cascade upsample path at C5's full size: subdivide_build on the 0.8 M parents, then
     subm_conv_gathered(x_parents, src, 3) 128 -> 64 with bias + SiLU on the fresh children's cache; every child row

@@ -1549,6 +1549,156 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   epilogue_tile<TM, TN>(acc, ew, ordT, nrows, co_w, bias8, e, a.Co, lane);
 }
 
+// 256 x 256 tile kernel with both operands in LDS (Co a multiple of 256, Ci a multiple of 32; opt-in with SPCONV_W8,
+// an evaluated alternative to k_conv_wide_dma): one workgroup per CU of 8 wavefronts (two per SIMD), wavefront
+// (wr, wc) owning rows wr*128 .. +128 x channels wc*64 .. +64 as 4 x 2 tiles of v_mfma_f32_32x32x16. A K stage is one
+// offset x 32 input channels: the 256 gathered rows (64 bytes each) and the 256 weight columns (64 bytes each) both go
+// global -> LDS by DMA into 3-slot rings (16 KB per slot and operand), two stages ahead, so each weight byte is
+// fetched once per 256 rows instead of once per 128. Slot layout: row (column) q's 16-byte piece p sits in unit
+// q*4 + (p ^ ((q >> 1) & 3)) (conflict-free fragment reads); the weight repack (k_pack_w8) stores the pieces in that
+// order so the weight DMA is one contiguous 16 KB block per stage. Every wavefront waits for its own DMAs (counted
+// vmcnt), then one barrier per stage publishes the slot and frees the one stage s+2 refills. Per-32-row-group skips
+// as in k_conv_wide_dma. The rings are six distinct LDS objects (slots named per unrolled stage) so that the
+// compiler can tell the DMA into one slot from the reads of another.
+template <bool F16>
+__global__ void __launch_bounds__(512, 1) k_conv_w8(ConvArgs a) {
+  constexpr int BM = 256, NT = 512, KC = 32, PU = KC / 8, SU = BM * PU;  // SU: 16-byte units per slot
+  constexpr int TM = 4, TN = 2;
+  __shared__ __attribute__((aligned(16))) u32x4 A0[SU], A1[SU], A2[SU], B0[SU], B1[SU], B2[SU];
+  __shared__ __attribute__((aligned(16))) uint32_t srcT[BM * 27];
+  __shared__ int ordT[BM];
+  __shared__ uint32_t gmask[BM / 32];
+  __shared__ int vlist[32];
+
+  const int tile = blockIdx.x;
+  if (tile >= a.tiles_m * a.tiles_n) return;
+  const int tm_ = a.tsched[tile / a.tiles_n], tn_ = tile % a.tiles_n;  // row tiles longest first
+  const int row0 = tm_ * BM, co0 = tn_ * 256;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), wr = wv >> 2, wc = wv & 3;
+  const int N = a.N, Ci = a.Ci, nkc = Ci / KC;
+
+  dma_tile_table<BM, NT>(a, row0, srcT, tid);
+  if (tid < BM) {
+    const int row = row0 + tid;
+    ordT[tid] = row < N ? a.order[row] : 0;
+    uint32_t gm = a.gs[row];  // padded rows have mask 0
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) gm |= (uint32_t)__shfl_xor((int)gm, d, 64);
+    if ((tid & 31) == 0) gmask[tid >> 5] = gm;
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  uint32_t mask = 0;
+#pragma unroll
+  for (int i = 0; i < BM / 32; i++) mask |= gmask[i];
+  const int nvv = __popc(mask), total = nvv * nkc;
+  if (tid < 27 && ((mask >> tid) & 1u)) vlist[__popc(mask & ((1u << tid) - 1u))] = tid;
+  uint32_t gms[TM];
+#pragma unroll
+  for (int i = 0; i < TM; i++) gms[i] = __builtin_amdgcn_readfirstlane(gmask[wr * TM + i]);
+  __syncthreads();
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes), rw = make_rsrc(a.w, a.w_bytes);
+  // this thread's DMA units (two A, two B per stage): unit u = k*NT + tid -> row/column u >> 2, slot u & 3, source
+  // piece slot ^ ((row >> 1) & 3)
+  uint32_t arow[2], apiece[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int u = k * NT + tid;
+    arow[k] = (uint32_t)(u >> 2);
+    apiece[k] = (uint32_t)((u & 3) ^ ((u >> 3) & 3));
+  }
+  auto issue = [&](int st, u32x4* As, u32x4* Bs) __attribute__((always_inline)) {
+    const int vi = st / nkc, kc = st % nkc;
+    const int v = __builtin_amdgcn_readfirstlane(vlist[vi]);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const uint32_t off = nbr_offset(srcT[arow[k] * 27 + v], (uint32_t)(Ci * 2)) + apiece[k] * 16u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)&As[k * NT + wv * 64], 16,
+                                               off, (uint32_t)(kc * KC * 2), 0, 0);
+    }
+    const uint32_t wbase = (uint32_t)(((tn_ * 27 + v) * nkc + kc) * SU) * 16u;
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)&Bs[k * NT + wv * 64], 16,
+                                               (uint32_t)(k * NT + tid) * 16u, wbase, 0, 0);
+  };
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int t = 0; t < TN; t++) acc[i][t] = f32x16{};
+  auto compute = [&](int st, const u32x4* As, const u32x4* Bs) __attribute__((always_inline)) {
+    const uint32_t vbit = 1u << __builtin_amdgcn_readfirstlane(vlist[st / nkc]);
+#pragma unroll
+    for (int j = 0; j < KC / 16; j++) {
+      const int p = 2 * j + h;
+      u32x4 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int r = wr * 128 + i * 32 + l32;
+        fa[i] = As[r * PU + (p ^ ((r >> 1) & 3))];
+      }
+#pragma unroll
+      for (int t = 0; t < TN; t++) {
+        const int c = wc * 64 + t * 32 + l32;
+        fb[t] = Bs[c * PU + (p ^ ((c >> 1) & 3))];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        if (gms[i] & vbit) {
+#pragma unroll
+          for (int t = 0; t < TN; t++) acc[i][t] = mfma32<F16>(fa[i], fb[t], acc[i][t]);
+        }
+    }
+  };
+  // stage s: wait for this thread's DMAs of stage s (the 4 of stage s+1 may stay in flight), barrier, refill the
+  // slot stage s-1 used with stage s+2, compute stage s
+  auto step = [&](int st, const u32x4* As, const u32x4* Bs, u32x4* Af, u32x4* Bf) __attribute__((always_inline)) {
+    if (st + 1 < total) wait_vmcnt<4>();
+    else wait_vmcnt<0>();
+    wg_barrier();
+    if (st + 2 < total) issue(st + 2, Af, Bf);
+    compute(st, As, Bs);
+  };
+  if (total > 0) {
+    issue(0, A0, B0);
+    if (total > 1) issue(1, A1, B1);
+    for (int st = 0; st < total; st += 3) {
+      step(st, A0, B0, A2, B2);
+      if (st + 1 >= total) break;
+      step(st + 1, A1, B1, A0, B0);
+      if (st + 2 >= total) break;
+      step(st + 2, A2, B2, A1, B1);
+    }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  // epilogue: a [32][72] fp32 staging area per wavefront in the idle rings (and the neighbour table for the last two)
+  static_assert(32 * 72 * 4 <= SU * 16 && 2 * 32 * 72 * 4 <= BM * 27 * 4, "epilogue staging fits");
+  float* ew = wv == 0 ? (float*)A0 : wv == 1 ? (float*)A1 : wv == 2 ? (float*)A2 : wv == 3 ? (float*)B0
+            : wv == 4 ? (float*)B1 : wv == 5 ? (float*)B2 : (float*)srcT + (wv - 6) * 32 * 72;
+  const int co_w = co0 + wc * 64;
+  float bias8[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) bias8[q] = a.bias ? a.bias[co_w + (lane & 7) * 8 + q] : 0.f;
+  const Epi e = make_epi(a);
+  epilogue_tile<TM, TN>(acc, ew, ordT + wr * 128, N - row0 - wr * 128, co_w, bias8, e, a.Co, lane);
+}
+
+// Weight repack for k_conv_w8: per (column tile of 256, offset, 32-channel chunk) one contiguous block of 1024
+// 16-byte units, unit u = column c (u >> 2) x slot (u & 3) holding channels ((u & 3) ^ ((c >> 1) & 3)) * 8 .. +8.
+__global__ void __launch_bounds__(256) k_pack_w8(const u32x4* __restrict__ w, u32x4* __restrict__ wp, int Ci) {
+  const int nkc = Ci / 32, kc = blockIdx.x, v = blockIdx.y, tn = blockIdx.z;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int u = k * 256 + threadIdx.x, c = u >> 2, piece = (u & 3) ^ ((c >> 1) & 3);
+    const int co = tn * 256 + c;
+    wp[(((i64)tn * 27 + v) * nkc + kc) * 1024 + u] = w[((i64)co * 27 + v) * (Ci / 8) + kc * 4 + piece];
+  }
+}
+
 // 256 x 256 tile kernel (Co a multiple of 256, Ci a multiple of 64): one workgroup per CU, 4 wavefronts, each
 // owning all 256 rows x its own 64 output channels (8 x 2 tiles of v_mfma_f32_32x32x16, 256 accumulator registers).
 //  * Bytes per flop: a K stage (one offset x 64 input channels) reads 256 gathered rows and 256 weight columns of
@@ -2046,6 +2196,11 @@ __global__ void __launch_bounds__(256) k_pack_w256(const u32x4* __restrict__ w, 
 // on C3 (same box, both with longest-first tile order): 0.947 ms against 0.918 -- it halves the weight bytes per
 // flop, but one wavefront per SIMD exposes every per-stage wait, and without group skipping it runs the tile's
 // union of offsets (1.18x the active pairs against 1.05x).
+// The 8-wavefront both-operands-in-LDS kernel (k_conv_w8) runs when SPCONV_W8 is set (read per call).
+bool w8_enabled() {
+  const char* e = getenv("SPCONV_W8");
+  return e && e[0] && e[0] != '0';
+}
 bool w256_enabled() {
   const char* e = getenv("SPCONV_W256");
   return e && e[0] && e[0] != '0';
@@ -2133,6 +2288,13 @@ void dispatch(const SpConvCfg& cfg, ConvArgs a) {
       case 3: return launch_narrow<F16, 3, 4>(a);
       default: return launch_narrow<F16, 4, 4>(a);
     }
+  }
+  if (a.Co % 256 == 0 && a.Ci % 32 == 0 && w8_enabled()) {
+    a.tiles_m = cdiv(a.N, 256);
+    a.tiles_n = a.Co / 256;
+    a.grid = a.tiles_m * a.tiles_n;
+    k_conv_w8<F16><<<a.grid, 512, 0, stream()>>>(a);
+    return;
   }
   // Fixed tiles per channel width (no autotune): BM = 128 sorted rows per tile.
   if (a.Co % 256 == 0 && a.Ci % 64 == 0 && w256_enabled()) return launch_w256<F16>(a);
@@ -2351,6 +2513,16 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
       a.rshift = shift;
       a.rmax = (int)std::min<i64>(M, INT32_MAX);
     }
+  } else if (Co % 256 == 0 && Ci % 32 == 0 && w8_enabled()) {  // 256 x 256 tiles, both operands through LDS
+    wpack = empty({(i64)Co * 27 * Ci}, x.dt);
+    k_pack_w8<<<dim3(Ci / 32, 27, Co / 256), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Ci);
+    a.w = wpack.ptr<uint16_t>();
+    const SpConvCache::RowTable& rt = c.row_table(-1);
+    if (row_map) mtbl = c.mapped_table(-1, *row_map, shift, M);
+    a.tbl = row_map ? mtbl.ptr<uint32_t>() : rt.tbl.ptr<uint32_t>();
+    a.gs = rt.gs.ptr<int32_t>();
+    a.tbl_bytes = (uint32_t)rt.tbl.bytes();
+    a.tsched = c.tile_schedule(-1, 256).ptr<int32_t>();
   } else if (Co % 256 == 0 && Ci % 64 == 0 && w256_enabled()) {  // 256 x 256 tiles: 4 KB weight blocks
     wpack = empty({(i64)Co * 27 * Ci}, x.dt);
     k_pack_w256<<<dim3(Ci / 64, 27, Co / 32), 256, 0, stream()>>>((const u32x4*)w.p, (u32x4*)wpack.p, Ci);
@@ -2378,6 +2550,7 @@ void conv_impl(const Tensor& x, const Tensor* row_map, int shift, const Tensor& 
   REQ(!ln || (ht && ht->host_spills() == 0), "the fused pre-activation needs the halo kernel with no spill tiles");
   // the generic kernel reads the reference's per-block offset masks (valid(B1)'s OR masks); the others do not
   if (!ht && !(Co == 64 && Ci <= 128) && !(Co % 256 == 0 && Ci % 64 == 0 && w256_enabled()) &&
+      !(Co % 256 == 0 && Ci % 32 == 0 && w8_enabled()) &&
       !(cfg.BK == 64 && Co % 128 == 0))
     a.code = c.block_masks(cfg.B1).ptr<uint32_t>();
   if (ln) {
