@@ -19,12 +19,14 @@ namespace {
 constexpr uint32_t EMPTY = 0xffffffffu;
 constexpr uint64_t HEMPTY = ~0ull;
 
-// Clears the live part of the table (mask + 1 slots; the mask is read from device memory when maskp is set),
-// grid-stride.
-__global__ void k_table_clear(ulonglong2* __restrict__ t, uint32_t mask, const uint32_t* __restrict__ maskp) {
+// Clears the live part of the table (mask + 1 slots; the mask is read from device memory when maskp is set) and
+// zeroes the zn words at z (the sort's first-pass counts and digit-sum slots), grid-stride.
+__global__ void k_table_clear(ulonglong2* __restrict__ t, uint32_t mask, const uint32_t* __restrict__ maskp,
+                              uint32_t* __restrict__ z, i64 zn) {
   const i64 cap = (i64)(maskp ? *maskp : mask) + 1;
   for (i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x; i < cap; i += (i64)gridDim.x * blockDim.x)
     t[i] = make_ulonglong2(HEMPTY, HEMPTY);
+  for (i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x; i < zn; i += (i64)gridDim.x * blockDim.x) z[i] = 0;
 }
 
 // ------------------------------------------------------------------------------------------ brick table
@@ -174,8 +176,10 @@ __global__ void __launch_bounds__(NVV) k_neighbors_vox(const int4* __restrict__ 
                                                        uint32_t mask0, const uint32_t* __restrict__ maskp,
                                                        const uint32_t* __restrict__ bricks,
                                                        uint32_t* __restrict__ nbr, int32_t* __restrict__ gray,
-                                                       uint32_t* __restrict__ bin, const uint32_t* __restrict__ ndev) {
+                                                       uint32_t* __restrict__ bin, const uint32_t* __restrict__ ndev,
+                                                       uint32_t* __restrict__ cnt0, int ntiles, int tile_keys) {
   __shared__ uint32_t rows[NVV * 27];
+  __shared__ uint32_t dcnt[512];
   if (ndev) n = min<i64>(n, *ndev);
   const uint32_t mask = maskp ? *maskp : mask0;
   const i64 v0 = (i64)blockIdx.x * NVV;
@@ -184,6 +188,9 @@ __global__ void __launch_bounds__(NVV) k_neighbors_vox(const int4* __restrict__ 
   const int tid = threadIdx.x;
   const bool live = tid < nv;
   const int4 q = c[v0 + (live ? tid : 0)];
+  dcnt[tid] = 0;
+  dcnt[tid + NVV] = 0;
+  __syncthreads();
   const int W4 = (W + 3) >> 2, H4 = (H + 3) >> 2, D4 = (D + 3) >> 2;
   const int ax = q.y & 3, ay = q.z & 3, az = q.w & 3;
   // per axis: the face the voxel sits on (-1 low, +1 high, 0 none)
@@ -256,8 +263,16 @@ __global__ void __launch_bounds__(NVV) k_neighbors_vox(const int4* __restrict__ 
     b ^= b >> 16;
     gray[v0 + tid] = (int32_t)g;
     bin[v0 + tid] = b;
+    atomicAdd(&dcnt[b & 511u], 1u);
   }
   __syncthreads();
+  // the sort's first pass counts its tiles' low 9-bit digits: this workgroup's voxels all lie in tile v0 / tile_keys
+  const i64 tile = v0 / tile_keys;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int d = k * NVV + tid;
+    if (dcnt[d]) atomicAdd(&cnt0[(i64)d * ntiles + tile], dcnt[d]);
+  }
   const int tot = nv * 27;
   uint32_t* o = nbr + v0 * 27;
 #pragma unroll
@@ -368,7 +383,11 @@ SpConvCache build_neighbors_impl(const int4* coords, i64 n, const uint32_t* ndev
     // 0.361 -> 0.323 ms; 8x no better)
     k_brick_mask<<<1, 1024, 0, s>>>(part.ptr<uint32_t>(), nb, cap, maskp, ndev, 4);
   }
-  k_table_clear<<<(int)std::min<i64>(cdiv((i64)cap, 256), 4096), 256, 0, s>>>(t, mask0, maskp);
+  // the sort's workspace: its first pass is counted by the neighbour kernel (slots and counts zeroed with the table)
+  SortWork sw = sort_work(n, 27);
+  REQ((sw.rch * 256) % NVV == 0, "sort tile of %d keys", sw.rch * 256);
+  k_table_clear<<<(int)std::min<i64>(cdiv(std::max<i64>((i64)cap, sw.zwords), 256), 4096), 256, 0, s>>>(
+      t, mask0, maskp, sw.buf.ptr<uint32_t>(), sw.zwords);
   // at most n occupied bricks: the table (capacity >= 2n) never fills. Brick records are indexed by the row of
   // the voxel that inserted the brick, so the record array has n slots (only occupied bricks' records are touched).
   Tensor bricks = empty({n * 64}, I32);
@@ -376,9 +395,9 @@ SpConvCache build_neighbors_impl(const int4* coords, i64 n, const uint32_t* ndev
   k_brick_fill<<<cdiv(n, 256), 256, 0, s>>>(coords, n, W4, H4, D4, t, mask0, maskp, bricks.ptr<uint32_t>(), ndev);
   k_neighbors_vox<<<cdiv(n, NVV), NVV, 0, s>>>(coords, n, W, H, D, t, mask0, maskp, bricks.ptr<uint32_t>(),
                                                c.nbr.ptr<uint32_t>(), c.gray.ptr<int32_t>(), bin.ptr<uint32_t>(),
-                                               ndev);
+                                               ndev, sw.counts(), sw.ntiles, sw.rch * 256);
   CK(hipGetLastError());
-  stable_argsort27(bin.ptr<uint32_t>(), n, c.sorted.ptr<int32_t>(), ndev);
+  stable_argsort27(bin.ptr<uint32_t>(), n, c.sorted.ptr<int32_t>(), ndev, &sw);
   c.W = W;
   c.H = H;
   c.D = D;

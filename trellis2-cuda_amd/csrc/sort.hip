@@ -109,7 +109,7 @@ __global__ void __launch_bounds__(RT) k_rs_scatter(const uint32_t* __restrict__ 
     if (i < n) {
       uint32_t d = (key[c] >> shift) & (NBUK - 1);
       uint32_t pos = cnt[wv][d] + rank[c];
-      kout[pos] = key[c];
+      if (kout) kout[pos] = key[c];  // the last pass writes only the values
       vout[pos] = val[c];
     }
   }
@@ -187,43 +187,58 @@ __global__ void __launch_bounds__(RT) k_rs_digit_scan(const uint32_t* __restrict
 }
 }  // namespace
 
+SortWork sort_work(i64 n, int bits) {
+  SortWork w;
+  w.passes = (bits + RBITS - 1) / RBITS;
+  w.rch = n >= (i64)RT * 16 * 512 ? 16 : (n >= (i64)RT * 8 * 512 ? 8 : 4);
+  w.ntiles = (int)std::max<i64>(cdiv(n, (i64)RT * w.rch), 1);
+  w.zwords = (i64)w.passes * NBUK * 2 + (i64)NBUK * w.ntiles;
+  // [digit-sum slots: passes x NBUK u64][first pass's counts: NBUK x ntiles][tile starts: NBUK x ntiles]; the
+  // slot words are even in number, so the 64-bit slots and everything after them stay 8-byte aligned
+  w.buf = empty({w.zwords + (i64)NBUK * w.ntiles}, I32);
+  return w;
+}
+
 void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bits, int32_t* vals_out,
-                       const uint32_t* ndev) {
+                       const uint32_t* ndev, SortWork* pre) {
   if (n <= 0) return;
   REQ(n < (1ll << 31), "sort size %lld", (long long)n);
   REQ(bits >= 1 && bits <= 32, "key bits %d", bits);
-  const int passes = (bits + RBITS - 1) / RBITS;
   hipStream_t s = stream();
   // SPCONV_SORT_SPIN_LIMIT overrides the digit-sum wait bound (0: every workgroup recomputes the lower digits' sums
   // itself; the tests use it to check that path)
   uint32_t spin_limit = kSpinLimit;
   if (const char* e = getenv("SPCONV_SORT_SPIN_LIMIT")) spin_limit = (uint32_t)strtoul(e, nullptr, 10);
+  SortWork own;
+  if (!pre) own = sort_work(n, bits);
+  SortWork& w = pre ? *pre : own;
+  REQ(w.passes == (bits + RBITS - 1) / RBITS && w.ntiles == (int)std::max<i64>(cdiv(n, (i64)RT * w.rch), 1),
+      "sort workspace made for another size");
+  const int passes = w.passes, rch = w.rch, ntiles = w.ntiles;
   Tensor kb0 = empty({n}, I32), kb1 = empty({n}, I32), vb0 = empty({n}, I32), vb1 = empty({n}, I32);
-  // ping-pong buffers; the last pass writes its values straight into vals_out
+  // ping-pong buffers; the last pass writes only its values, straight into vals_out
   const uint32_t* kin = keys;
   const int32_t* vin = vals;
   auto outs = [&](int p, uint32_t*& kout, int32_t*& vout) {
-    kout = (p & 1) ? kb1.ptr<uint32_t>() : kb0.ptr<uint32_t>();
+    kout = p + 1 == passes ? nullptr : ((p & 1) ? kb1.ptr<uint32_t>() : kb0.ptr<uint32_t>());
     vout = p + 1 == passes ? vals_out : ((p & 1) ? vb1.ptr<int32_t>() : vb0.ptr<int32_t>());
   };
-  const int rch = n >= (i64)RT * 16 * 512 ? 16 : (n >= (i64)RT * 8 * 512 ? 8 : 4);
-  const int ntiles = (int)cdiv(n, (i64)RT * rch);
-  const i64 nh = (i64)NBUK * ntiles, swords = (i64)passes * NBUK * 2;
-  // per-tile counts, tile starts, digit-sum slots (nh is even: the 64-bit slots stay 8-byte aligned)
-  Tensor hist = empty({2 * nh + swords}, I32);
-  uint64_t* dsum = (uint64_t*)(hist.ptr<uint32_t>() + 2 * nh);
-  uint32_t* h = hist.ptr<uint32_t>();
-  uint32_t* st = h + nh;
+  const i64 swords = (i64)passes * NBUK * 2;
+  uint64_t* dsum = (uint64_t*)w.buf.ptr<uint32_t>();
+  uint32_t* h = w.buf.ptr<uint32_t>() + swords;
+  uint32_t* st = h + (i64)NBUK * ntiles;
   for (int p = 0; p < passes; p++) {
     uint32_t* kout;
     int32_t* vout;
     outs(p, kout, vout);
     const int shift = p * RBITS;
-    uint32_t* z = p == 0 ? (uint32_t*)dsum : nullptr;  // the first count kernel zeroes every pass's digit sums
-    const int zn = (int)swords;
-    if (rch == 16) k_rs_count<16><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
-    else if (rch == 8) k_rs_count<8><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
-    else k_rs_count<4><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
+    if (p > 0 || !pre) {  // a caller-made workspace arrives with the first pass counted and the slots zeroed
+      uint32_t* z = p == 0 ? (uint32_t*)dsum : nullptr;  // the first count kernel zeroes every pass's digit sums
+      const int zn = (int)swords;
+      if (rch == 16) k_rs_count<16><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
+      else if (rch == 8) k_rs_count<8><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
+      else k_rs_count<4><<<ntiles, RT, 0, s>>>(kin, n, shift, h, ntiles, z, zn, ndev);
+    }
     k_rs_digit_scan<<<NBUK, RT, 0, s>>>(h, st, dsum + p * NBUK, ntiles, spin_limit, ndev, RT * rch);
     if (rch == 16) k_rs_scatter<16><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles, ndev);
     else if (rch == 8) k_rs_scatter<8><<<ntiles, RT, 0, s>>>(kin, vin, kout, vout, n, shift, st, ntiles, ndev);
@@ -234,6 +249,6 @@ void stable_sort_pairs(const uint32_t* keys, const int32_t* vals, i64 n, int bit
   CK(hipGetLastError());
 }
 
-void stable_argsort27(const uint32_t* keys, i64 n, int32_t* order, const uint32_t* ndev) {
-  stable_sort_pairs(keys, nullptr, n, 27, order, ndev);
+void stable_argsort27(const uint32_t* keys, i64 n, int32_t* order, const uint32_t* ndev, SortWork* pre) {
+  stable_sort_pairs(keys, nullptr, n, 27, order, ndev, pre);
 }
