@@ -56,6 +56,37 @@ def host_cpu():
             "model": model}
 
 
+def gemm_ceiling(torch, settle_s, reps):
+    """The vendor BLAS's dense bf16 GEMM (8192^3, torch.mm) after the same settle as the conv steps (batches of 10
+    until at least settle_s seconds have passed and a batch is no faster than the one before), then `reps` timed
+    calls: the sustained MFMA ceiling of this box to set beside the conv kernels."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    ga = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
+    gb = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
+    gc = torch.empty((8192, 8192), device=dev, dtype=torch.bfloat16)
+
+    def batch(k):
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record(stream)
+        for _ in range(k):
+            torch.mm(ga, gb, out=gc)
+        eb.record(stream)
+        torch.cuda.synchronize()
+        return ea.elapsed_time(eb) / k
+    batch(2)
+    t0, prev = time.perf_counter(), None
+    while True:
+        cur = batch(10)
+        el = time.perf_counter() - t0
+        if (el >= settle_s and prev is not None and cur >= 0.995 * prev) or el >= 5 * max(settle_s, 0.2):
+            break
+        prev = cur
+    ms = batch(reps)
+    del ga, gb, gc
+    return {"gemm_ms": round(ms, 4), "bf16_gemm_TFLOPs": round(2 * 8192 ** 3 / (ms * 1e-3) / 1e12, 1)}
+
+
 def cpu_conv_baseline(oracle, np, x, w, b, res, act, nbr_u32, seconds, cpu):
     """Times the oracle conv (fp32, multithreaded over output rows) on a random row sample sized to ~`seconds`."""
     n = nbr_u32.shape[0]
@@ -470,6 +501,9 @@ def main():
                     help="only the one config: no other configs, upsample-block or ConvNeXt-tail extras (profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy (the counter calibration used by bench_profile.py)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only time the vendor dense bf16 GEMM ceiling (8192^3 torch.mm, settled; --steps calls): the "
+                         "profiling command of the GEMM reference summary")
     ap.add_argument("--kmap-only", action="store_true",
                     help="only time the kernel-map build of the workload (--steps builds; the profiling command of the "
                          "kernel-map summary)")
@@ -481,6 +515,10 @@ def main():
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
+        return
+    if args.gemm_only:
+        import torch
+        print(json.dumps(gemm_ceiling(torch, args.settle, args.steps)), flush=True)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box has one GPU).",
@@ -524,11 +562,9 @@ def main():
         dst = torch.empty_like(src)
         copy_gbs = 2 * (1 << 30) / (timed(lambda: dst.copy_(src), 5) * 1e-3) / 1e9
         del src, dst
-        ga = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
-        gb = torch.randn((8192, 8192), device=dev).to(torch.bfloat16)
-        gemm_tf = 2 * 8192 ** 3 / (timed(lambda: torch.mm(ga, gb), 10) * 1e-3) / 1e12
-        del ga, gb
-        measured = {"hbm_copy_GBps": round(copy_gbs, 1), "bf16_gemm_TFLOPs": round(gemm_tf, 1)}
+        g = gemm_ceiling(torch, args.settle, 20)
+        gemm_tf = g["bf16_gemm_TFLOPs"]
+        measured = {"hbm_copy_GBps": round(copy_gbs, 1), "bf16_gemm_TFLOPs": gemm_tf, "bf16_gemm_settled": True}
         r = head["roofline"]
         measured["frac_of_measured"] = round(r["achieved"] / (gemm_tf if r["bound"] == "mfma" else copy_gbs), 4)
 
