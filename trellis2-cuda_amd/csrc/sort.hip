@@ -4,7 +4,8 @@
 //
 // Three launches per pass over tiles of 256 x RCH keys (RCH = 4, 8 or 16, so there are at least ~512 tiles when
 // the input allows it):
-//   count      : per-tile digit counts, digit-major [512][ntiles] (the first one also zeroes the digit-sum slots)
+//   count      : per-tile digit counts, digit-major [512][ntiles] (the first one also zeroes the digit-sum slots;
+//                a producer that already holds the keys may count the first pass itself, see SortWork)
 //   digit scan : one workgroup per digit sums its row and publishes the sum; its start is the sum of the lower
 //                digits' published sums (read back all at once); the row is scanned to exclusive tile starts.
 //                One launch instead of a device-wide scan's three.
