@@ -661,11 +661,15 @@ def test_c5_conv_skip_full(gpu):
     skip = qp[(s >> 3)[:, None], cols]
     nbr, _, _, _ = oracle.build_neighbors(ch.cpu().numpy())
     ref = oracle.conv(qh, qw, b, nbr, res=skip, act=1)
-    compare(y, ref, "bf16", "c5 conv skip (fused)")
     yr, y2r = y.float().cpu().numpy(), y2.float().cpu().numpy()
     rel2 = np.linalg.norm(y2r - ref) / np.linalg.norm(ref)
     assert rel2 <= 2e-3 and np.all(np.abs(y2r - ref) <= np.maximum(2e-2, 2 * ulp(ref, "bf16"))), \
         f"conv + add_skip: rel-L2 {rel2:.3g}"
+    if os.environ.get("SPCONV_NO_HALO", "0") not in ("", "0"):
+        # without the halo kernel subm_conv_skip is the conv, then add_skip: the same two roundings as y2
+        assert torch.equal(y, y2), "subm_conv_skip without the halo kernel is conv + add_skip"
+        return
+    compare(y, ref, "bf16", "c5 conv skip (fused)")
     assert np.linalg.norm(yr - ref) <= np.linalg.norm(y2r - ref) * 1.01, "one rounding should not be worse than two"
 
 

@@ -840,14 +840,29 @@ __global__ void __launch_bounds__(256, LITE ? 3 : 1) k_conv_narrow(ConvArgs a) {
   // gathers of offset list entry vi into ra (groups without that offset skip their loads)
   auto gather = [&](int vi, u32x4 (&ra)[G][S]) __attribute__((always_inline)) {
     const int v = __builtin_amdgcn_readfirstlane(vlist[vi]);
-    uint32_t off[G];  // all groups' row offsets first: one LDS round trip, not one per group
+    uint32_t nb[G];  // all groups' neighbour rows first: one LDS round trip, not one per group
 #pragma unroll
-    for (int i = 0; i < G; i++) off[i] = nbr_offset(srcT[(wv * (16 * G) + i * 16 + r16) * SR + v], CI * 2) + q4 * (S * 16);
+    for (int i = 0; i < G; i++) nb[i] = srcT[(wv * (16 * G) + i * 16 + r16) * SR + v];
 #pragma unroll
     for (int i = 0; i < G; i++) {
       if ((gms[i] >> v) & 1u) {
+        if constexpr (LITE) {
+          // lanes of rows without this neighbour skip the load (exec-masked) instead of reading out of range: at
+          // Ci = 128 half the rows of an active group lack its offset (C5 children: 0.854 -> 0.839 ms; at Ci = 64
+          // no gain, 0.901 -> 0.905)
+          const uint32_t off = nb[i] * (CI * 2) + q4 * (S * 16);
+          if (nb[i] != EMPTY) {
 #pragma unroll
-        for (int m = 0; m < S; m++) ra[i][m] = __builtin_amdgcn_raw_buffer_load_b128(rx, off[i] + m * 16, 0, 0);
+            for (int m = 0; m < S; m++) ra[i][m] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + m * 16, 0, 0);
+          } else {
+#pragma unroll
+            for (int m = 0; m < S; m++) ra[i][m] = u32x4{0, 0, 0, 0};
+          }
+        } else {
+          const uint32_t off = nbr_offset(nb[i], CI * 2) + q4 * (S * 16);
+#pragma unroll
+          for (int m = 0; m < S; m++) ra[i][m] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + m * 16, 0, 0);
+        }
       }
     }
   };
