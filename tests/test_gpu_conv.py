@@ -161,6 +161,15 @@ def test_configs_all_rows(gpu, name):
     run_case(gpu, c, cfg.ci, cfg.co, act=act, res_dt=res, seed=cfg.seed)
 
 
+@pytest.mark.parametrize("r,co", [(40, 256), (45, 512), (65, 256), (60, 512)])
+def test_wide_xcd_runs(gpu, r, co):
+    """The longest-first schedule of the wide kernel dealt to the XCDs in runs of consecutive tiles, at tile counts
+    whose last block of runs is partial in different ways (312, 798, 833 and 1416 tiles of 128 rows x 256 columns:
+    remainders 56, 30, 65 and 8 of 128): every output row against the oracle, so a tile computed twice or never
+    fails."""
+    run_case(gpu, shell(r), 256, co, act=1, res_dt="bf16", seed=r)
+
+
 def test_halo128_children(gpu, monkeypatch):
     """The halo kernel at Ci = 128 (opt-in, SPCONV_HALO128): two K chunks per offset, 128-row windows, spill tiles
     to the gathering kernel; c5-style children, every row against the oracle, plain and gathered."""
