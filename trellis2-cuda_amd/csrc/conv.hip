@@ -77,6 +77,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
 }
 
+// Logical tile of workgroup g when tiles are dealt to the XCDs in runs (workgroup ids go to the 8 XCDs in turn):
+// each XCD takes run consecutive tiles of every 8 * run, in order; a last, partial block of rem < 8 * run tiles gives
+// XCD x rem / 8 of them (one more for x < rem % 8). A bijection of [0, T); g >= T has no tile (-1).
+__device__ __forceinline__ int xcd_run_tile(int g, int T, int run) {
+  if (g >= T) return -1;
+  const int bs = 8 * run, base = g / bs * bs, r = g - base, x = r % 8, k = r / 8, rem = min(bs, T - base);
+  return base + x * (rem / 8) + min(x, rem % 8) + k;
+}
+
 // vmcnt-only s_waitcnt (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14])
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -147,7 +156,10 @@ struct ConvArgs {
   // (C2, 768 -> 768: 32 MB of weights, past L2; 0.298 -> 0.287 ms)
   int tnmaj;
   int xt0[9], xk[8], xpart0[8], xs;
-  int xblk;  // longest-first schedule: each XCD takes xblk consecutive tiles of every 8*xblk (0: round-robin)
+  // Tiles dealt to the XCDs in runs: each XCD takes xblk consecutive tiles of every 8*xblk, in order (k_conv_wide_dma's
+  // longest-first schedule, k_conv_halo's windows). 0: one tile per XCD in turn (wide), one contiguous range per XCD
+  // (halo).
+  int xblk;
 };
 
 template <bool F16, int BM, int BN, int WGM, int WGN, int KC>
@@ -1061,14 +1073,8 @@ __global__ void __launch_bounds__(256, OCC) k_conv_halo(ConvArgs a) {
   const int g = blockIdx.x, per = a.grid / 8;
   // tiles in runs of xblk consecutive windows per XCD (each XCD takes xblk of every 8 * xblk in order), so that the
   // eight XCDs work on nearby windows at any time; xblk = 0: each XCD walks one contiguous range
-  int tile = (g % 8) * per + g / 8;
-  if (a.xblk > 0) {
-    const int TT = a.tiles_m;
-    if (g >= TT) return;
-    const int BS = 8 * a.xblk, base = g / BS * BS, r = g - base, x = r % 8, k = r / 8, rem = min(BS, TT - base);
-    tile = base + x * (rem / 8) + min(x, rem % 8) + k;
-  }
-  if (tile >= a.tiles_m) return;
+  const int tile = a.xblk > 0 ? xcd_run_tile(g, a.tiles_m, a.xblk) : (g % 8) * per + g / 8;
+  if (tile < 0 || tile >= a.tiles_m) return;
   const int row0 = tile * B;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
   const int wr = wv / WC, wc = wv % WC;
@@ -1414,14 +1420,8 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
     // (SpConvCache::tile_schedule), so every XCD gets an even share of long and short tiles and the launch ends on
     // short ones (the XCD-contiguous walk below leaves each XCD its densest tiles for last)
     // (in runs of xblk consecutive tiles per XCD: each XCD takes xblk of every 8 * xblk in order)
-    logical = g;
-    if (a.xblk > 0) {
-      const int T = a.tiles_m * a.tiles_n;
-      if (g >= T) return;
-      const int BS = 8 * a.xblk, base = g / BS * BS, r = g - base, x = r % 8, k = r / 8, rem = min(BS, T - base);
-      const int q = rem / 8, e = rem % 8;
-      logical = base + x * q + min(x, e) + k;
-    }
+    logical = a.xblk > 0 ? xcd_run_tile(g, a.tiles_m * a.tiles_n, a.xblk) : g;
+    if (logical < 0) return;
   } else {
     logical = (g % 8) * per + g / 8;
   }
