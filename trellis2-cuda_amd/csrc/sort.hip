@@ -2,7 +2,7 @@
 // permutation (src/spconv.cu:47-52: cub::DeviceRadixSort::SortPairs(bin -> iota), stable, bits 0..32; bin < 2^27
 // so bits 27..31 are all zero and sorting 27 bits gives the same order).
 //
-// Three launches per pass over tiles of 256 x RCH keys (RCH = 4, 8 or 16, so there are at least ~512 tiles when
+// Three launches per pass over tiles of 256 x RCH keys (RCH = 4, 8 or 16, so there are at least ~900 tiles when
 // the input allows it):
 //   count      : per-tile digit counts, digit-major [512][ntiles] (the first one also zeroes the digit-sum slots;
 //                a producer that already holds the keys may count the first pass itself, see SortWork)
@@ -191,7 +191,9 @@ __global__ void __launch_bounds__(RT) k_rs_digit_scan(const uint32_t* __restrict
 SortWork sort_work(i64 n, int bits) {
   SortWork w;
   w.passes = (bits + RBITS - 1) / RBITS;
-  w.rch = n >= (i64)RT * 16 * 512 ? 16 : (n >= (i64)RT * 8 * 512 ? 8 : 4);
+  // the largest tile that still leaves ~900 tiles (interleaved builds, one box: C3 0.390 M keys best at 4, C4 3.76 M
+  // at 16 (8: +3%), C5's children 2.15 M at 8 (16: +1.2%))
+  w.rch = n >= (i64)RT * 16 * 900 ? 16 : (n >= (i64)RT * 8 * 900 ? 8 : 4);
   w.ntiles = (int)std::max<i64>(cdiv(n, (i64)RT * w.rch), 1);
   w.zwords = (i64)w.passes * NBUK * 2 + (i64)NBUK * w.ntiles;
   // [digit-sum slots: passes x NBUK u64][first pass's counts: NBUK x ntiles][tile starts: NBUK x ntiles]; the
