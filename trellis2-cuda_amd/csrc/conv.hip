@@ -1472,15 +1472,19 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
   const uint32_t wslice = (uint32_t)((co0 >> 6) + wn) * 27u * (uint32_t)nkc;
   const uint32_t wlane = (uint32_t)lane * 16u;
 
-  int avi = s0 / nkc, akc = s0 % nkc, bvi = avi, bkc = akc, cvi = avi, ckc = akc;
+  // K stages run channel block outer, offset inner: stage s = (kc = s / nvv, offset entry vi = s % nvv). A row chunk
+  // gathered for one offset is then gathered again for the next offset's (one voxel over) neighbours one stage
+  // later instead of nkc stages later, while it is still in L2: C3 0.837 -> 0.826 ms, C2 0.297 -> 0.293 (two
+  // interleaved runs; each output's fp32 sum runs over (kc, v) in that order).
+  int avi = s0 % nvv, akc = s0 / nvv, bvi = avi, bkc = akc, cvi = avi, ckc = akc;
   auto next = [&](int& vi, int& kc) __attribute__((always_inline)) {
-    const bool wrap = kc + 1 == nkc;
-    kc = wrap ? 0 : kc + 1;
-    vi += wrap ? 1 : 0;
+    const bool wrap = vi + 1 == nvv;
+    vi = wrap ? 0 : vi + 1;
+    kc += wrap ? 1 : 0;
   };
   // DMA addresses of the next A stage (offset entry avi, channel block akc; clamped to the last stage)
   auto a_offsets = [&](uint32_t (&off)[AL], int& ka) __attribute__((always_inline)) {
-    const bool live = avi < nvv;
+    const bool live = avi < nvv && akc < nkc;
     const int va = __builtin_amdgcn_readfirstlane(vlist[live ? avi : nvv - 1]);
     ka = __builtin_amdgcn_readfirstlane((live ? akc : nkc - 1) * KC * 2);
     next(avi, akc);
@@ -1492,7 +1496,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) k_conv_wide_dma(ConvAr
                                              16, off, ka, 0, 0);
   };
   auto b_base = [&]() __attribute__((always_inline)) {
-    const bool live = bvi < nvv;
+    const bool live = bvi < nvv && bkc < nkc;
     const int vb = __builtin_amdgcn_readfirstlane(vlist[live ? bvi : nvv - 1]);
     const int kb = live ? bkc : nkc - 1;
     next(bvi, bkc);
