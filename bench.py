@@ -426,6 +426,50 @@ DECODER_LEVELS = [(11, 1024, 1024), (11, 1024, 4096), (14, 512, 512), (14, 512, 
                   (16, 256, 1024), (19, 128, 128), (19, 128, 512), (21, 64, 64)]
 
 
+def upsample_only(args, torch, np, sp, W):
+    """The cascade upsample block of a subdivision workload (c5) alone, --steps times after one untimed block: c2s
+    subdivision + the children's map (subdivide_build, no host sync between them) -> the children's conv on the fresh
+    cache, reading the parents' rows through the c2s map (first-call schedules included). The profiling command of
+    the upsample-block summary (bench_profile.py --upsample)."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    cfg = W.CONFIGS[args.config]
+    if not cfg.subdivide:
+        sys.exit(f"--upsample-only needs a subdivision workload (c5), not {args.config}")
+    coords = W.shell_coords(cfg)
+    par = torch.from_numpy(coords).to(dev)
+    lg = W.keep_logits(len(coords), cfg.keep_frac, cfg.seed)
+    lgt = torch.from_numpy(lg.view(np.int16)).to(dev).view(torch.float16)
+    g = torch.Generator(device=dev)
+    g.manual_seed(cfg.seed)
+    xp = torch.randn((len(coords), cfg.ci), generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn((cfg.co, 27, cfg.ci), generator=g, device=dev) / (27 * cfg.ci) ** 0.5).to(torch.bfloat16)
+    b = torch.randn((cfg.co,), generator=g, device=dev) * 0.1
+    act = sp.ACT_SILU if "silu" in cfg.epilogue else sp.ACT_NONE
+    parts = {"kmap": [], "conv": [], "total": []}
+    m = 0
+    for i in range(1 + args.steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record(stream)
+        ch, src, cc = sp.subdivide_build(par, lgt)
+        ev[1].record(stream)
+        y = torch.empty((len(ch), cfg.co), dtype=torch.bfloat16, device=dev)
+        sp.subm_conv_gathered(xp, src, 3, w, b, cc, act=act, out=y)
+        ev[2].record(stream)
+        torch.cuda.synchronize()
+        m = len(ch)
+        if i:
+            parts["kmap"].append(ev[0].elapsed_time(ev[1]))
+            parts["conv"].append(ev[1].elapsed_time(ev[2]))
+            parts["total"].append(ev[0].elapsed_time(ev[2]))
+        del ch, src, cc, y
+    return {"workload": f"{args.config} upsample block: {len(coords)} parents -> {m} children, "
+                        f"{cfg.ci}->{cfg.co} gathered conv", "parents": len(coords), "children": m,
+            "blocks": args.steps, **{k + "_ms": round(float(np.median(v)), 4) for k, v in parts.items()},
+            "note": "kmap_ms = subdivide_build (subdivision + children's map); conv_ms = the gathered conv on the "
+                    "fresh cache, first-call schedules included; HIP events, median"}
+
+
 def decoder_levels(torch, np, sp, W):
     """Conv kernel time at each decoder level's shape on a seeded shell of ~2^L voxels (the c3 recipe with the grid
     scaled to the voxel count), bias + SiLU, bf16; HIP events around the conv kernels, median of 20 calls."""
@@ -504,6 +548,9 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="only time the vendor dense bf16 GEMM ceiling (8192^3 torch.mm, settled; --steps calls): the "
                          "profiling command of the GEMM reference summary")
+    ap.add_argument("--upsample-only", action="store_true",
+                    help="only time the cascade upsample block of a subdivision workload (--config c5; --steps "
+                         "blocks): the profiling command of the upsample-block summary")
     ap.add_argument("--kmap-only", action="store_true",
                     help="only time the kernel-map build of the workload (--steps builds; the profiling command of the "
                          "kernel-map summary)")
@@ -537,6 +584,9 @@ def main():
     cpu = host_cpu()
     if args.kmap_only:
         print(json.dumps(measure(args.config, args, torch, np, sp, W, cpu, False, 0, False)), flush=True)
+        return
+    if args.upsample_only:
+        print(json.dumps(upsample_only(args, torch, np, sp, W)), flush=True)
         return
     extras = not args.no_extras
     head = measure(args.config, args, torch, np, sp, W, cpu, not args.no_cpu, args.cpu_seconds, extras)

@@ -9,6 +9,8 @@ counter/actual ratio scales the conv kernel's counters into bytes. It writes, un
   <kernel>_<config>.md       the commands and the figures behind the documented roofline numbers
   traffic_<config>.json      HBM bytes per launch of the dominant kernel (read by bench.py)
 
+With --upsample it profiles the cascade upsample block of c5 (bench.py --upsample-only): every kernel of the
+subdivision, the children's map and the gathered conv, per block -> profiles/upsample_block_<config>.md.
 With --kmap it profiles the kernel-map build instead (bench.py --kmap-only): per-kernel time and HBM bytes of every
 build kernel -> profiles/kmap_build_<config>.md. With --gemm it profiles the vendor dense bf16 GEMM (bench.py
 --gemm-only) with the same clock / MFMA-busy counters -> profiles/gemm_bf16_8192.md.
@@ -114,6 +116,48 @@ def kmap_profile(args, out, py, rp, copy, prof):
     print(json.dumps({"config": args.config, "kernels": per, "sum_us": tot_us, "sum_bytes": tot_b, "plain": kb}))
 
 
+def upsample_profile(args, out, py, rp, prof):
+    """Cascade upsample block (bench.py --upsample-only): every kernel of subdivide_build and of the gathered conv on
+    the fresh cache (first-call schedules included), summed per block."""
+    blocks = args.steps + 1  # bench.py --upsample-only runs one untimed block, then --steps timed ones
+    cmd = [py, os.path.join(ROOT, "bench.py"), "--config", args.config, "--steps", str(args.steps), "--upsample-only"]
+    run(cmd, 120, f"{out}/plain.log")
+    plain = json.loads([l for l in open(f"{out}/plain.log") if l.startswith("{")][-1])
+    run(rp + ["--kernel-trace", "--stats", "-d", f"{out}/trace", "--"] + cmd, 300, f"{out}/trace.log")
+    rows = []
+    for r in csv_rows(f"{out}/trace", "kernel_stats.csv"):
+        m = re.search(r"(k_\w+)", r["Name"])
+        if not m:
+            continue  # torch's input generation and copies
+        rows.append((m.group(1), int(r["Calls"]), float(r["AverageNs"]), float(r["TotalDurationNs"])))
+    agg = {}
+    for k, calls, avg, tot in rows:  # template instances of one kernel summed under its name
+        a = agg.setdefault(k, [0, 0.0])
+        a[0] += calls
+        a[1] += tot
+    md = [f"# Cascade upsample block on workload {args.config}: {plain['parents']} parents -> {plain['children']} "
+          "children", "",
+          "Commands (run from the repository root on an MI355X box, each under `timeout -s KILL`):", "",
+          "```", "rocprofv3 " + " ".join(rp[1:]) + " --kernel-trace --stats -d <out>/trace -- " + rel(cmd, py), "```",
+          f"(generated by `python bench_profile.py --upsample --config {args.config}`; {blocks} blocks per command: "
+          "subdivide_build, then the gathered conv on the fresh cache with its first-call schedules)", "",
+          "| kernel | dispatches per block | average us | us per block | share |", "|---|---|---|---|---|"]
+    tot_us = sum(v[1] for v in agg.values()) / 1e3 / blocks
+    for k, (calls, tot) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        per = tot / 1e3 / blocks
+        md.append(f"| `{k}` | {calls / blocks:g} | {tot / 1e3 / calls:.1f} | {per:.1f} | {100 * per / tot_us:.1f}% |")
+    md += ["", f"Sum of the block's kernels: {tot_us:.1f} us per block.",
+           f"Without the profiler the same command times a block (HIP events, median of {args.steps}) at "
+           f"{plain['total_ms'] * 1e3:.1f} us: subdivide_build {plain['kmap_ms'] * 1e3:.1f} us, the conv on the fresh "
+           f"cache {plain['conv_ms'] * 1e3:.1f} us. The kernel sum can exceed the block time where the spill-tile "
+           "kernel of a 64-channel conv runs on a second stream beside the main one; here the conv is 128 -> 64 "
+           "(the gathering kernel, one stream)."]
+    with open(os.path.join(prof, f"upsample_block_{args.config}.md"), "w") as f:
+        f.write("\n".join(md) + "\n")
+    print(json.dumps({"config": args.config, "kernels_us_per_block": {k: v[1] / 1e3 / blocks for k, v in agg.items()},
+                      "sum_us": tot_us, "plain": plain}))
+
+
 def rel(cmd, py):
     return " ".join(os.path.relpath(c, ROOT) if c.startswith(ROOT) else ("python3" if c == py else c) for c in cmd)
 
@@ -176,6 +220,8 @@ def main():
     ap.add_argument("--config", default="c3")
     ap.add_argument("--kmap", action="store_true", help="profile the kernel-map build instead of the conv step")
     ap.add_argument("--gemm", action="store_true", help="profile the vendor dense bf16 GEMM ceiling instead")
+    ap.add_argument("--upsample", action="store_true",
+                    help="profile the cascade upsample block of a subdivision workload (--config c5) instead")
     ap.add_argument("--out", default=os.path.join(tempfile.gettempdir(), "spconv_prof"))
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--profiles-dir", default=os.path.join(ROOT, "profiles"),
@@ -191,6 +237,11 @@ def main():
     if args.kmap:
         os.makedirs(args.profiles_dir, exist_ok=True)
         return kmap_profile(args, out, py, rp, copy, args.profiles_dir)
+    if args.upsample:
+        out = os.path.join(args.out, "upsample_" + args.config)
+        os.makedirs(out, exist_ok=True)
+        os.makedirs(args.profiles_dir, exist_ok=True)
+        return upsample_profile(args, out, py, rp, args.profiles_dir)
     if args.gemm:
         out = os.path.join(args.out, "gemm")
         os.makedirs(out, exist_ok=True)
